@@ -1,0 +1,343 @@
+"""QIPACK W4A4 / W4A16 linear benchmark on one MI355X.
+
+A step is one pass of one Qwen-Image MMDiT dual-stream block's linears at
+1024x1024 (image stream M = 4096 tokens, text stream M = 256 tokens; per
+stream to_q, to_k, to_v, to_out 3072x3072, MLP up 3072->12288 with fused
+GELU-tanh, down 12288->3072), W4A4 with H256/g64: every
+distinct input is quantised online (Q/K/V share one quantisation, as the
+reference's reuse_input does) and all seven GEMMs run.  value = block TOPS
+(2*M*N*K int ops per GEMM, quantiser work not counted).  The same pass with
+W4A16 weights (config 2) and the M=1/M=2 modulation GEMV (config 4) are
+reported beside it.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "qwen-image-cplus_amd"))
+
+HIDDEN, MLP = 3072, 12288
+STREAMS = {"image": 4096, "text": 256}
+MODULATION_N = 18432
+PEAK_INT8_OPS = 5.0e15      # MI355X dense int8 MFMA
+PEAK_FP16_FLOPS = 2.5e15    # MI355X dense fp16 MFMA
+PEAK_HBM = 8.0e12           # MI355X HBM3E bytes/s
+TRAFFIC_FILE = ROOT / "profiles" / "w4a4_gemm_traffic.json"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def block_shapes():
+    """(name, N, K) of one stream's block linears."""
+    return [("to_q", HIDDEN, HIDDEN), ("to_k", HIDDEN, HIDDEN), ("to_v", HIDDEN, HIDDEN),
+            ("to_out", HIDDEN, HIDDEN), ("mlp_up", MLP, HIDDEN), ("mlp_down", HIDDEN, MLP)]
+
+
+def block_ops() -> float:
+    params = sum(n * k for _, n, k in block_shapes())
+    return 2.0 * params * sum(STREAMS.values())
+
+
+class Block:
+    """Random-init weights of one block (both streams), packed on the device."""
+
+    def __init__(self, scheme: int, seed: int):
+        import torch
+        import qwen_image_hip as q
+
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        self.layers = {}
+        for stream in STREAMS:
+            for name, n, k in block_shapes():
+                w = (torch.randn((n, k), generator=g, device="cuda") * 0.02).half()
+                # W4A4 packs use the clip search; W4A16 packs do not (the
+                # reference's published packs, README.md:38).
+                self.layers[(stream, name)] = q.PackedLinear.from_fp16(scheme, w, clip=(scheme == q.SCHEME_W4A4_H256))
+                del w
+        torch.cuda.synchronize()
+
+
+def heavy_tailed(m, k, g):
+    """Student-t (3 dof) fp16 activations, 1% of channels scaled by 20."""
+    import torch
+
+    z = torch.randn((m, k), generator=g, device="cuda")
+    chi2 = sum(torch.randn((m, k), generator=g, device="cuda") ** 2 for _ in range(3))
+    t = z / torch.sqrt(chi2 / 3.0)
+    idx = torch.randperm(k, generator=g, device="cuda")[: -(-k // 100)]
+    t[:, idx] *= 20.0
+    return t.half()
+
+
+class StepW4A4:
+    def __init__(self, block: Block, seed: int):
+        import torch
+        from qwen_image_hip import ops
+
+        self.ops = ops
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        self.block = block
+        self.bufs = {}
+        for stream, m in STREAMS.items():
+            b = {
+                "x_qkv": heavy_tailed(m, HIDDEN, g), "x_out": heavy_tailed(m, HIDDEN, g),
+                "x_mlp": heavy_tailed(m, HIDDEN, g),
+                "codes": torch.empty((m, MLP // 2), dtype=torch.uint8, device="cuda"),
+                "scales": torch.empty((m, MLP // 64), dtype=torch.float16, device="cuda"),
+                "y": torch.empty((m, HIDDEN), dtype=torch.float16, device="cuda"),
+                "h": torch.empty((m, MLP), dtype=torch.float16, device="cuda"),
+            }
+            self.bufs[stream] = b
+
+    def codes(self, b, m, k):
+        return b["codes"].view(-1)[: m * k // 2].view(m, k // 2), b["scales"].view(-1)[: m * k // 64].view(m, k // 64)
+
+    def __call__(self):
+        ops = self.ops
+        for stream, m in STREAMS.items():
+            b = self.bufs[stream]
+            L = lambda name: self.block.layers[(stream, name)]  # noqa: E731
+            c, s = self.codes(b, m, HIDDEN)
+            ops.quantize_activations(b["x_qkv"], c, s)
+            for name in ("to_q", "to_k", "to_v"):
+                ops.w4a4_gemm(c, s, L(name).tiled_codes, L(name).tiled_scales, out_dtype=ops.torch.float16, y=b["y"])
+            ops.quantize_activations(b["x_out"], c, s)
+            ops.w4a4_gemm(c, s, L("to_out").tiled_codes, L("to_out").tiled_scales, out_dtype=ops.torch.float16, y=b["y"])
+            ops.quantize_activations(b["x_mlp"], c, s)
+            ops.w4a4_gemm(c, s, L("mlp_up").tiled_codes, L("mlp_up").tiled_scales, out_dtype=ops.torch.float16,
+                          gelu=True, y=b["h"])
+            c2, s2 = self.codes(b, m, MLP)
+            ops.quantize_activations(b["h"], c2, s2)
+            ops.w4a4_gemm(c2, s2, L("mlp_down").tiled_codes, L("mlp_down").tiled_scales, out_dtype=ops.torch.float16,
+                          y=b["y"])
+
+
+class StepW4A16:
+    def __init__(self, block: Block, seed: int):
+        import torch
+        from qwen_image_hip import ops
+
+        self.ops = ops
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        self.block = block
+        self.bufs = {}
+        for stream, m in STREAMS.items():
+            self.bufs[stream] = {
+                "x": torch.randn((m, HIDDEN), generator=g, device="cuda").half(),
+                "y": torch.empty((m, HIDDEN), dtype=torch.float16, device="cuda"),
+                "h": torch.empty((m, MLP), dtype=torch.float16, device="cuda"),
+            }
+
+    def __call__(self):
+        ops = self.ops
+        for stream, m in STREAMS.items():
+            b = self.bufs[stream]
+            L = lambda name: self.block.layers[(stream, name)]  # noqa: E731
+            for name in ("to_q", "to_k", "to_v", "to_out"):
+                ops.w4a16_gemm(b["x"], L(name).tiled_codes, L(name).tiled_scales, out_dtype=ops.torch.float16, y=b["y"])
+            ops.w4a16_gemm(b["x"], L("mlp_up").tiled_codes, L("mlp_up").tiled_scales, out_dtype=ops.torch.float16,
+                           gelu=True, y=b["h"])
+            ops.w4a16_gemm(b["h"], L("mlp_down").tiled_codes, L("mlp_down").tiled_scales, out_dtype=ops.torch.float16,
+                           y=b["y"])
+
+
+def time_fn(fn, iters, warmup):
+    """Mean ms per call with HIP events on the current stream (the one every
+    op is launched on)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(iters):
+        fn()
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) / iters
+
+
+def dominant_kernel(block: Block, step: StepW4A4):
+    """The image-stream to_q W4A4 GEMM (M=4096, N=K=3072) timed alone."""
+    from qwen_image_hip import ops
+    import torch
+
+    m = STREAMS["image"]
+    b = step.bufs["image"]
+    c, s = step.codes(b, m, HIDDEN)
+    ops.quantize_activations(b["x_qkv"], c, s)
+    L = block.layers[("image", "to_q")]
+    fn = lambda: ops.w4a4_gemm(c, s, L.tiled_codes, L.tiled_scales, out_dtype=torch.float16, y=b["y"])  # noqa: E731
+    ms = time_fn(fn, 50, 5)
+    ops_per_launch = 2.0 * m * HIDDEN * HIDDEN
+    return ms, ops_per_launch
+
+
+def bench_gemv(iters=200):
+    """M=1 and M=2 modulation GEMV 3072->18432 over a rotating pool of weight
+    copies larger than the 256 MB MALL, so every launch reads HBM."""
+    import torch
+    import qwen_image_hip as q
+    from qwen_image_hip import ops
+
+    n, k = MODULATION_N, HIDDEN
+    g = torch.Generator(device="cuda")
+    g.manual_seed(77)
+    pool = []
+    for i in range(10):
+        w = (torch.randn((n, k), generator=g, device="cuda") * 0.02).half()
+        pool.append(q.PackedLinear.from_fp16(q.SCHEME_W4A16, w))
+        del w
+    bytes_per = n * k // 2 + n * (k // 64) * 4  # codes + scales + minimums
+    out = {}
+    for m in (1, 2):
+        x = torch.randn((m, k), generator=g, device="cuda").half()
+        y = torch.empty((m, n), dtype=torch.float16, device="cuda")
+        idx = [0]
+
+        def fn():
+            r = pool[idx[0] % len(pool)]
+            idx[0] += 1
+            ops.w4a16_gemv(x, r.tiled_codes, r.tiled_scales, out_dtype=torch.float16, y=y)
+
+        ms = time_fn(fn, iters, 20)
+        total = bytes_per + m * k * 2 + m * n * 2
+        out[f"m{m}"] = {"us": round(ms * 1e3, 3), "GB_s": round(total / (ms * 1e-3) / 1e9, 1),
+                        "frac_hbm": round(total / (ms * 1e-3) / PEAK_HBM, 4), "bytes": total}
+    return out
+
+
+def cpu_baseline(seconds_target=12.0):
+    """The CPU oracle (C, OpenMP over the host cores) on a bounded sample of
+    the same workload: activation quantisation + W4A4 GEMM of the to_q shape
+    (N = K = 3072) over a slice of image-stream rows; TOPS = 2*M*N*K / time."""
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT / "oracle"))
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle
+    from _data import heavy_tailed as ht, weights_f16
+
+    oracle.lib()
+    w = weights_f16(HIDDEN, HIDDEN, 5)
+    wc, ws, _ = oracle.quantize_matrix(w, 6, clip=True)
+    rows = 16
+    while True:
+        x = ht(rows, HIDDEN, 6)
+        t0 = time.perf_counter()
+        ac, as_ = oracle.quantize_activations(x)
+        oracle.w4a4_gemm(ac, as_, wc, ws)
+        dt = time.perf_counter() - t0
+        if dt * 4 >= seconds_target or rows >= 4096:
+            break
+        rows = min(4096, rows * max(2, int(seconds_target / max(dt, 1e-3) / 4)))
+    ops_ = 2.0 * rows * HIDDEN * HIDDEN
+    return {"value": round(ops_ / dt / 1e12, 6), "unit": "TOPS", "cores": oracle.num_threads(), "kind": "port",
+            "sample": f"W4A4 quantise + GEMM, M={rows} of the image stream, N=K={HIDDEN} (to_q), "
+                      f"{dt:.2f} s on {os.cpu_count()} host CPUs ({platform.processor() or platform.machine()})"}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="only the headline W4A4 block")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    import qwen_image_hip as q
+
+    q.load()
+    torch.cuda.set_device(0)
+    log("packing W4A4 block weights")
+    blk4 = Block(q.SCHEME_W4A4_H256, 1)
+    step4 = StepW4A4(blk4, 2)
+    for _ in range(args.warmup):
+        step4()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        step4()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = start.elapsed_time(stop) / args.steps
+    tops = block_ops() / (ms_step * 1e-3) / 1e12
+    log(f"w4a4 block: {ms_step:.3f} ms/step, {tops:.1f} TOPS (wall {wall:.3f} s)")
+
+    dom_ms, dom_ops = dominant_kernel(blk4, step4)
+    achieved = dom_ops / (dom_ms * 1e-3) / 1e12
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        try:
+            traffic = json.loads(TRAFFIC_FILE.read_text()).get("bytes_per_launch")
+        except (ValueError, OSError):
+            traffic = None
+    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_OPS / 1e12, "unit": "TFLOP/s",
+                "frac": round(achieved * 1e12 / PEAK_INT8_OPS, 4), "traffic": traffic,
+                "kernel": "w4a4_gemm_kernel M=4096 N=3072 K=3072 (int8 MFMA ops)", "ms_per_launch": round(dom_ms, 4)}
+    del step4, blk4
+    torch.cuda.empty_cache()
+
+    extra = {}
+    if not args.no_extra:
+        log("packing W4A16 block weights")
+        blk16 = Block(q.SCHEME_W4A16, 3)
+        step16 = StepW4A16(blk16, 4)
+        ms16 = time_fn(step16, args.steps, args.warmup)
+        tf16 = block_ops() / (ms16 * 1e-3) / 1e12
+        extra["w4a16_block"] = {"ms_per_step": round(ms16, 4), "TFLOP_s": round(tf16, 1),
+                                "frac_fp16_peak": round(tf16 * 1e12 / PEAK_FP16_FLOPS, 4)}
+        log(f"w4a16 block: {ms16:.3f} ms/step, {tf16:.1f} TFLOP/s")
+        del step16, blk16
+        torch.cuda.empty_cache()
+        extra["modulation_gemv"] = bench_gemv()
+        log(f"gemv: {extra['modulation_gemv']}")
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline")
+        cpu = cpu_baseline()
+        log(f"cpu: {cpu}")
+
+    line = {
+        "metric": "QIPACK W4A4/W4A16 linear TOPS + % roofline, MMDiT block @1024^2 (M=4352)",
+        "value": round(tops, 2), "unit": "TOPS", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int4xint4->int32 (int8 MFMA), fp32 epilogue, fp16 out", "data": "synthetic",
+        "config": {"workload": "W4A4 H256 g64 one MMDiT dual-stream block linears (config 3): image M=4096 + "
+                               "text M=256, hidden 3072, MLP 12288, heavy-tailed fp16 activations, online quantiser",
+                   "global_batch": 1, "seq_len": sum(STREAMS.values()), "parallelism": "single-gpu"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    line.update(extra)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

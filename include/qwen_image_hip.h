@@ -1,0 +1,141 @@
+/*
+ * qwen_image_hip.h -- C ABI of the MI355X (gfx950) QIPACK INT4 linear backend.
+ *
+ * Conventions (shared with the reference's libqwen_image_cuda, whose entry
+ * points are cited as file:line in netdur/qwen-image-cplus 0.2.5):
+ *   - every pointer argument is a DEVICE pointer owned by the caller; nothing
+ *     on this path allocates or frees device memory;
+ *   - every function returns a hipError_t as int, 0 = success; shape or
+ *     argument violations return hipErrorInvalidValue (1) before any launch;
+ *     otherwise the launch status (hipGetLastError) is returned and the work
+ *     completes asynchronously;
+ *   - the four reference-named entry points run on the null (legacy default)
+ *     stream, as the reference does; every qi_hip_* entry point takes a
+ *     hipStream_t passed as void * (NULL = null stream);
+ *   - layouts are row-major, little-endian; fp16 is IEEE binary16 passed as
+ *     void * (uint16_t storage); "G" is K / 64 groups.
+ *
+ * Weight layouts.  A QIPACK record stores codes [N, K/2] (even k in the low
+ * nibble), fp16 scales [N, G] and, for W4A16, fp16 minimums [N, G]
+ * (int4_pack.cplus:6-15).  The qi_hip_relayout_* functions permute those
+ * arrays once, at upload, into the MFMA-tile order the *_tiled kernels read:
+ *
+ *   W4A4 tiled codes   [N/16][G][64 lanes][8 bytes]
+ *                      lane l carries row 16*t + (l % 16), bytes
+ *                      [8*(l/16), 8*(l/16) + 8) of that row's 32-byte group.
+ *   W4A4 tiled scales  [N/16][G][16] fp16
+ *   W4A16 tiled codes  [N/16][G][64 lanes][8 bytes]
+ *                      lane l carries row 16*t + (l % 16), bytes
+ *                      [4q, 4q+4) and [16+4q, 16+4q+4), q = l / 16.
+ *   W4A16 tiled scales [N/16][G][16][2] fp16 pairs (scale, minimum)
+ *
+ * The byte contents are unchanged (a permutation); the *_inverse functions
+ * restore the QIPACK arrays exactly.  A tiled buffer has the same byte size
+ * as the source arrays (scales and minimums are interleaved into one array of
+ * twice the size for W4A16).
+ */
+#ifndef QWEN_IMAGE_HIP_H
+#define QWEN_IMAGE_HIP_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ABI version of this header; bumped on any signature change. */
+#define QI_HIP_ABI_VERSION 1
+int qi_hip_abi_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Reference-named entry points (drop-in for libqwen_image_cuda).
+ * ------------------------------------------------------------------------- */
+
+/* Replaces qwen_image_cuda/cuda/gemm.cu:54 (qi_w4a4_quantize_activations),
+ * bound at qwen_image_cuda/src/cuda.cplus:53-54.  x f32 [m, k] -> codes
+ * [m, k/2] (H256-rotated, signed int4, even k low nibble), scales fp16
+ * [m, k/64] = fp16(max(absmax / 7, 2^-24)).  Requires k % 256 == 0 (the
+ * reference leaves k unchecked; this build rejects it) and m >= 0. */
+int qi_w4a4_quantize_activations(const float *x, void *codes, void *scales, int m, int k);
+
+/* Replaces gemm.cu:183 (qi_w4a4_gemm), bound at cuda.cplus:55-56.
+ * y f32 [m, n] = sum_g float(P_g) * (sa[m,g] * sw[n,g]) with P_g the exact
+ * int32 per-group partial of the int4 codes.  Weights in QIPACK layout (not
+ * tiled).  Requires m % 128 == 0, n % 128 == 0, k % 256 == 0, exactly as the
+ * reference does. */
+int qi_w4a4_gemm(const void *a_codes, const void *a_scales, const void *w_codes, const void *w_scales,
+                 float *y, int m, int n, int k);
+
+/* Replaces gemm.cu:262 (qi_w4a16_gemm), bound at cuda.cplus:57-58.
+ * y f32 [m, n] = x_half [m, k] . W^T with W = fp16(fmaf(code, scale, min)).
+ * Weights in QIPACK layout.  Requires m % 128 == 0, n % 128 == 0,
+ * k % 64 == 0, exactly as the reference does. */
+int qi_w4a16_gemm(const void *x_half, const void *codes, const void *scales, const void *minimums, float *y,
+                  int m, int n, int k);
+
+/* Replaces qwen_image_cuda/cuda/ops.cu:209 (qi_f32_to_f16), bound at
+ * cuda.cplus:45-46.  Round-to-nearest-even f32 -> fp16. */
+int qi_f32_to_f16(const float *source, void *out, unsigned long long count);
+
+/* ---------------------------------------------------------------------------
+ * Extensions: stream-taking forms, tiled weights, fused epilogues, GEMV.
+ * No reference counterpart unless cited.
+ * ------------------------------------------------------------------------- */
+
+/* Stream-taking forms of the four reference entry points (same semantics). */
+int qi_hip_w4a4_quantize_activations(const float *x, void *codes, void *scales, int m, int k, void *stream);
+int qi_hip_f32_to_f16(const float *source, void *out, unsigned long long count, void *stream);
+
+/* fp16-input activation quantiser, same arithmetic after exact widening
+ * (the reference's bench twin, qwen_image_cuda/cuda/bench/bench_w4a4.cu:30-66). */
+int qi_hip_w4a4_quantize_activations_f16(const void *x_half, void *codes, void *scales, int m, int k,
+                                         void *stream);
+
+/* One-time re-layout at upload (see layouts above).  n % 16 == 0 and
+ * k % 256 == 0 (W4A4) or k % 64 == 0 (W4A16). */
+int qi_hip_relayout_w4a4(const void *codes, const void *scales, void *tiled_codes, void *tiled_scales, int n,
+                         int k, void *stream);
+int qi_hip_relayout_w4a4_inverse(const void *tiled_codes, const void *tiled_scales, void *codes, void *scales,
+                                 int n, int k, void *stream);
+int qi_hip_relayout_w4a16(const void *codes, const void *scales, const void *minimums, void *tiled_codes,
+                          void *tiled_scales, int n, int k, void *stream);
+int qi_hip_relayout_w4a16_inverse(const void *tiled_codes, const void *tiled_scales, void *codes, void *scales,
+                                  void *minimums, int n, int k, void *stream);
+
+/* Output element type and fused epilogue for the *_tiled GEMMs and GEMV.
+ * The epilogue computes, in fp32, v = acc (+ bias[n]) then optionally
+ * gelu_tanh(v) (ops.cu:156-160 formula), then stores fp32 or RNE fp16. */
+#define QI_HIP_OUT_F32 0
+#define QI_HIP_OUT_F16 1
+#define QI_HIP_EPILOGUE_NONE 0
+#define QI_HIP_EPILOGUE_GELU_TANH 1
+
+/* W4A4 GEMM on tiled weights.  a_codes/a_scales as produced by the
+ * quantiser (QIPACK activation layout [m, k/2], [m, k/64]).  bias is an
+ * fp32 [n] vector or NULL.  Any m >= 1; n % 16 == 0; k % 256 == 0. */
+int qi_hip_w4a4_gemm_tiled(const void *a_codes, const void *a_scales, const void *w_tiled_codes,
+                           const void *w_tiled_scales, const float *bias, void *y, int out_type, int epilogue,
+                           int m, int n, int k, void *stream);
+
+/* W4A16 GEMM on tiled weights.  x_half fp16 [m, k]; any m >= 1;
+ * n % 16 == 0; k % 64 == 0.  Dispatches to the GEMV kernel for m <= 16. */
+int qi_hip_w4a16_gemm_tiled(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
+                            const float *bias, void *y, int out_type, int epilogue, int m, int n, int k,
+                            void *stream);
+
+/* Bandwidth-bound W4A16 GEMV for 1 <= m <= 16 (the adaLN / timestep
+ * modulation linears).  Same arithmetic and layouts as above.  The
+ * reference runs these linears as BF16 -> fp32 SGEMM
+ * (qwen_image_cuda/src/transformer.cplus:716-730, cuda/blas.cu:138-142). */
+int qi_hip_w4a16_gemv(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
+                      const float *bias, void *y, int out_type, int epilogue, int m, int n, int k, void *stream);
+
+/* Device-side QIPACK quantiser (int4_pack.cplus:237-468 arithmetic, bit-exact):
+ * w_half fp16 [n, k] -> QIPACK arrays.  scheme 5 = W4A16 affine (minimums
+ * required), scheme 6 = W4A4 H256 symmetric (minimums ignored).  group must
+ * be 64; clip selects the 7-candidate range-shrink search. */
+int qi_hip_pack_weights(const void *w_half, void *codes, void *scales, void *minimums, int n, int k, int scheme,
+                        int clip, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QWEN_IMAGE_HIP_H */

@@ -1,0 +1,77 @@
+// Shared device helpers for the gfx950 QIPACK linear kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/qwen_image_hip.h"
+
+#define QI_API extern "C" __attribute__((visibility("default")))
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
+namespace qi {
+
+constexpr int GROUP = 64;      // QIPACK v6 group size along K
+constexpr int WAVE = 64;       // CDNA wavefront
+
+inline hipStream_t stream_of(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int launch_status() { return static_cast<int>(hipGetLastError()); }
+
+constexpr int kInvalid = static_cast<int>(hipErrorInvalidValue);
+
+// fp16 bits <-> float on the device.  __builtin bit casts keep this exact.
+__device__ __forceinline__ float h2f(uint16_t bits) {
+    _Float16 h = __builtin_bit_cast(_Float16, bits);
+    return static_cast<float>(h);
+}
+// Round-to-nearest-even float -> fp16 bits (v_cvt_f16_f32 under the default
+// RNE mode register).
+__device__ __forceinline__ uint16_t f2h(float v) {
+    _Float16 h = static_cast<_Float16>(v);
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+// ops.cu:156-160 (gelu_tanh_kernel) formula, evaluated in fp32.
+__device__ __forceinline__ float gelu_tanh(float v) {
+    return 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum16(float v) {
+    // Sum over the four 16-lane groups (lanes l, l+16, l+32, l+48).
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+// Signed int4 nibbles -> int8 lanes scaled by 16 (value 16*q in each byte).
+// lo: the low nibble of every byte moved up; hi: the high nibble kept in
+// place.  A 16*q operand on both MFMA sides yields 256*P exactly.
+__device__ __forceinline__ int nib_lo16(uint32_t x) { return static_cast<int>((x << 4) & 0xF0F0F0F0u); }
+__device__ __forceinline__ int nib_hi16(uint32_t x) { return static_cast<int>(x & 0xF0F0F0F0u); }
+
+// Epilogue store of one fp32 value.
+__device__ __forceinline__ void store_out(void *y, size_t index, float v, int out_type) {
+    if (out_type == QI_HIP_OUT_F16)
+        reinterpret_cast<uint16_t *>(y)[index] = f2h(v);
+    else
+        reinterpret_cast<float *>(y)[index] = v;
+}
+
+__device__ __forceinline__ float epilogue(float v, const float *bias, int col, int epi) {
+    if (bias) v += bias[col];
+    if (epi == QI_HIP_EPILOGUE_GELU_TANH) v = gelu_tanh(v);
+    return v;
+}
+
+}  // namespace qi

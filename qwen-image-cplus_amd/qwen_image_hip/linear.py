@@ -1,0 +1,113 @@
+"""Host-side mirror of the reference's backend linear-op interface.
+
+The reference engine calls one function per linear layer,
+``transformer::linear(model, work, index, input, output, rows, reuse_input)``
+(qwen_image_cuda/src/transformer.cplus:669-713), which dispatches on the pack
+record's scheme:
+
+* scheme 6 (W4A4 H256): quantise ``input`` into ``work.codes`` /
+  ``work.code_scales`` unless ``reuse_input``, then ``qi_w4a4_gemm``;
+* scheme 5 (W4A16): convert ``input`` to fp16 into ``work.halves`` unless
+  ``reuse_input``, then ``qi_w4a16_gemm``.
+
+This module keeps that shape.  ``PackedLinear`` is one uploaded INT4 record,
+re-laid out once into MFMA-tile order (the load-time hook the reference's
+``transformer::load``, transformer.cplus:342-501, would call).  ``Work`` holds
+the activation scratch the reference sizes in ``allocate_work``
+(transformer.cplus:638-667).  Unlike the reference, rows need not be a
+multiple of 128, outputs may be fp16 with a fused bias/GELU epilogue, and
+m <= 16 dispatches to the bandwidth-bound GEMV.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import ops
+
+SCHEME_W4A16 = 5
+SCHEME_W4A4_H256 = 6
+
+
+@dataclass
+class PackedLinear:
+    """One INT4 block matrix resident in HBM in tiled order."""
+
+    scheme: int
+    n: int
+    k: int
+    tiled_codes: torch.Tensor
+    tiled_scales: torch.Tensor
+    bias: torch.Tensor | None = None  # fp32 [n] or None (the reference has none)
+
+    @classmethod
+    def from_qipack(cls, scheme: int, codes: torch.Tensor, scales: torch.Tensor,
+                    minimums: torch.Tensor | None = None, bias: torch.Tensor | None = None) -> "PackedLinear":
+        """Upload hook: re-lay the QIPACK arrays of one record (device tensors)."""
+        n, half_k = codes.shape
+        if scheme == SCHEME_W4A4_H256:
+            tc, ts = ops.relayout_w4a4(codes, scales)
+        elif scheme == SCHEME_W4A16:
+            if minimums is None:
+                raise ValueError("W4A16 records carry a minimums (zeros) array")
+            tc, ts = ops.relayout_w4a16(codes, scales, minimums)
+        else:
+            raise ValueError(f"unsupported INT4 scheme {scheme}")
+        return cls(scheme, n, half_k * 2, tc, ts, bias)
+
+    @classmethod
+    def from_fp16(cls, scheme: int, w_half: torch.Tensor, clip: bool = False,
+                  bias: torch.Tensor | None = None) -> "PackedLinear":
+        """Quantise an fp16 [N, K] matrix with the QIPACK quantiser, then re-lay it."""
+        codes, scales, mins = ops.pack_weights(w_half, scheme, clip)
+        return cls.from_qipack(scheme, codes, scales, mins, bias)
+
+
+class Work:
+    """Activation scratch shared by consecutive linears (the reference's Work)."""
+
+    def __init__(self, rows_max: int, k_max: int, device: torch.device | str = "cuda"):
+        self.rows_max = rows_max
+        self.k_max = k_max
+        self.codes = torch.empty(rows_max * k_max // 2, dtype=torch.uint8, device=device)
+        self.code_scales = torch.empty(rows_max * k_max // ops.GROUP, dtype=torch.float16, device=device)
+        self.halves = torch.empty(rows_max * k_max, dtype=torch.float16, device=device)
+
+    def views(self, rows: int, k: int):
+        if rows > self.rows_max or k > self.k_max:
+            raise ValueError("work buffers are smaller than this linear")
+        return (self.codes[: rows * k // 2].view(rows, k // 2),
+                self.code_scales[: rows * k // ops.GROUP].view(rows, k // ops.GROUP),
+                self.halves[: rows * k].view(rows, k))
+
+
+def linear(record: PackedLinear, work: Work, input: torch.Tensor, output: torch.Tensor | None = None,
+           rows: int | None = None, reuse_input: bool = False, gelu: bool = False,
+           out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """output[rows, N] = input[rows, K] . W^T (+ bias, GELU) for one record.
+
+    ``input`` is fp32 (the engine's activations) or fp16.  ``reuse_input``
+    skips the quantisation / conversion when the previous linear already
+    processed the same input (Q/K/V and gate/up in the reference).
+    """
+    rows = input.shape[0] if rows is None else rows
+    k = record.k
+    if input.shape[-1] != k:
+        raise ValueError(f"input width {input.shape[-1]} != record inputs {k}")
+    codes, code_scales, halves = work.views(rows, k)
+    if record.scheme == SCHEME_W4A4_H256:
+        if not reuse_input:
+            ops.quantize_activations(input[:rows], codes, code_scales)
+        return ops.w4a4_gemm(codes, code_scales, record.tiled_codes, record.tiled_scales, record.bias,
+                             out_dtype, gelu, output)
+    if record.scheme == SCHEME_W4A16:
+        if input.dtype == torch.float16:
+            x_half = input[:rows]
+        else:
+            if not reuse_input:
+                ops.f32_to_f16(input[:rows], halves)
+            x_half = halves
+        return ops.w4a16_gemm(x_half, record.tiled_codes, record.tiled_scales, record.bias, out_dtype, gelu,
+                              output)
+    raise ValueError(f"unsupported scheme {record.scheme}")

@@ -1,0 +1,189 @@
+"""Torch-tensor wrappers over the C ABI.  torch supplies device memory and the
+current HIP stream; every computation happens in the gfx950 kernels.
+
+Shapes and dtypes follow the QIPACK arrays: codes are uint8 [N, K/2], scales
+and minimums are fp16 [N, K/64]; activation codes/scales use the same layout
+with M rows.  fp16 tensors are passed as torch.float16.
+"""
+from __future__ import annotations
+
+import torch
+
+from ._lib import check, load
+
+OUT_F32 = 0
+OUT_F16 = 1
+EPILOGUE_NONE = 0
+EPILOGUE_GELU_TANH = 1
+GROUP = 64
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("qwen_image_hip ops take device tensors")
+    if not t.is_contiguous():
+        raise ValueError("qwen_image_hip ops take contiguous tensors")
+    return t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _empty(shape, dtype, like: torch.Tensor) -> torch.Tensor:
+    return torch.empty(shape, dtype=dtype, device=like.device)
+
+
+# ----------------------------------------------------------- activations --
+
+
+def quantize_activations(x: torch.Tensor, codes: torch.Tensor | None = None, scales: torch.Tensor | None = None):
+    """H256-rotate and int4-quantise rows of x (fp32 or fp16) -> (codes, scales).
+
+    Reference: qwen_image_cuda/cuda/gemm.cu:22-57.
+    """
+    m, k = x.shape
+    codes = codes if codes is not None else _empty((m, k // 2), torch.uint8, x)
+    scales = scales if scales is not None else _empty((m, k // GROUP), torch.float16, x)
+    lib = load()
+    if x.dtype == torch.float32:
+        st = lib.qi_hip_w4a4_quantize_activations(_ptr(x), _ptr(codes), _ptr(scales), m, k, _stream())
+    elif x.dtype == torch.float16:
+        st = lib.qi_hip_w4a4_quantize_activations_f16(_ptr(x), _ptr(codes), _ptr(scales), m, k, _stream())
+    else:
+        raise TypeError("activations must be float32 or float16")
+    check(st, "activation quantization")
+    return codes, scales
+
+
+def f32_to_f16(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """RNE fp32 -> fp16 (reference qwen_image_cuda/cuda/ops.cu:204-212)."""
+    out = out if out is not None else _empty(x.shape, torch.float16, x)
+    check(load().qi_hip_f32_to_f16(_ptr(x), _ptr(out), x.numel(), _stream()), "activation conversion")
+    return out
+
+
+# ------------------------------------------------------------------ packing --
+
+
+def pack_weights(w_half: torch.Tensor, scheme: int, clip: bool = False):
+    """QIPACK-quantise an fp16 [N, K] matrix on the device.
+
+    scheme 5 -> (codes, scales, minimums) W4A16 affine; scheme 6 -> (codes,
+    scales, None) W4A4 with the H256 rotation.  Same arithmetic as the
+    reference packer (qwen_image_cuda/src/int4_pack.cplus:237-468).
+    """
+    n, k = w_half.shape
+    codes = _empty((n, k // 2), torch.uint8, w_half)
+    scales = _empty((n, k // GROUP), torch.float16, w_half)
+    mins = _empty((n, k // GROUP), torch.float16, w_half) if scheme == 5 else None
+    st = load().qi_hip_pack_weights(_ptr(w_half), _ptr(codes), _ptr(scales), _ptr(mins), n, k, scheme,
+                                    1 if clip else 0, _stream())
+    check(st, "weight packing")
+    return codes, scales, mins
+
+
+def relayout_w4a4(codes: torch.Tensor, scales: torch.Tensor):
+    n, half_k = codes.shape
+    k = half_k * 2
+    tc = torch.empty_like(codes)
+    ts = torch.empty_like(scales)
+    check(load().qi_hip_relayout_w4a4(_ptr(codes), _ptr(scales), _ptr(tc), _ptr(ts), n, k, _stream()), "relayout")
+    return tc, ts
+
+
+def relayout_w4a4_inverse(tiled_codes: torch.Tensor, tiled_scales: torch.Tensor):
+    n, half_k = tiled_codes.shape
+    k = half_k * 2
+    c = torch.empty_like(tiled_codes)
+    s = torch.empty_like(tiled_scales)
+    check(load().qi_hip_relayout_w4a4_inverse(_ptr(tiled_codes), _ptr(tiled_scales), _ptr(c), _ptr(s), n, k,
+                                              _stream()), "relayout inverse")
+    return c, s
+
+
+def relayout_w4a16(codes: torch.Tensor, scales: torch.Tensor, minimums: torch.Tensor):
+    n, half_k = codes.shape
+    k = half_k * 2
+    tc = torch.empty_like(codes)
+    ts = _empty((n, 2 * (k // GROUP)), torch.float16, codes)
+    check(load().qi_hip_relayout_w4a16(_ptr(codes), _ptr(scales), _ptr(minimums), _ptr(tc), _ptr(ts), n, k,
+                                       _stream()), "relayout")
+    return tc, ts
+
+
+def relayout_w4a16_inverse(tiled_codes: torch.Tensor, tiled_scales: torch.Tensor):
+    n, half_k = tiled_codes.shape
+    k = half_k * 2
+    c = torch.empty_like(tiled_codes)
+    s = _empty((n, k // GROUP), torch.float16, tiled_codes)
+    mn = _empty((n, k // GROUP), torch.float16, tiled_codes)
+    check(load().qi_hip_relayout_w4a16_inverse(_ptr(tiled_codes), _ptr(tiled_scales), _ptr(c), _ptr(s), _ptr(mn),
+                                               n, k, _stream()), "relayout inverse")
+    return c, s, mn
+
+
+# -------------------------------------------------------------------- GEMMs --
+
+
+def w4a4_gemm_reference(a_codes, a_scales, w_codes, w_scales, y=None):
+    """Reference-ABI W4A4 GEMM (QIPACK weight layout, fp32 out, null stream).
+
+    Reference: qwen_image_cuda/cuda/gemm.cu:183-189.
+    """
+    m, n, k = a_codes.shape[0], w_codes.shape[0], a_codes.shape[1] * 2
+    y = y if y is not None else _empty((m, n), torch.float32, a_codes)
+    torch.cuda.current_stream().synchronize()
+    check(load().qi_w4a4_gemm(_ptr(a_codes), _ptr(a_scales), _ptr(w_codes), _ptr(w_scales), _ptr(y), m, n, k),
+          "w4a4 gemm")
+    torch.cuda.synchronize()
+    return y
+
+
+def w4a16_gemm_reference(x_half, codes, scales, minimums, y=None):
+    """Reference-ABI W4A16 GEMM (gemm.cu:262-268), null stream."""
+    m, k = x_half.shape
+    n = codes.shape[0]
+    y = y if y is not None else _empty((m, n), torch.float32, x_half)
+    torch.cuda.current_stream().synchronize()
+    check(load().qi_w4a16_gemm(_ptr(x_half), _ptr(codes), _ptr(scales), _ptr(minimums), _ptr(y), m, n, k),
+          "w4a16 gemm")
+    torch.cuda.synchronize()
+    return y
+
+
+def w4a4_gemm(a_codes, a_scales, w_tiled_codes, w_tiled_scales, bias=None, out_dtype=torch.float32,
+              gelu=False, y=None):
+    m, n, k = a_codes.shape[0], w_tiled_codes.shape[0], a_codes.shape[1] * 2
+    out_type = OUT_F16 if out_dtype == torch.float16 else OUT_F32
+    y = y if y is not None else _empty((m, n), out_dtype, a_codes)
+    st = load().qi_hip_w4a4_gemm_tiled(_ptr(a_codes), _ptr(a_scales), _ptr(w_tiled_codes), _ptr(w_tiled_scales),
+                                       _ptr(bias), _ptr(y), out_type, EPILOGUE_GELU_TANH if gelu else EPILOGUE_NONE,
+                                       m, n, k, _stream())
+    check(st, "w4a4 gemm")
+    return y
+
+
+def w4a16_gemm(x_half, w_tiled_codes, w_tiled_scales, bias=None, out_dtype=torch.float32, gelu=False, y=None):
+    m, k = x_half.shape
+    n = w_tiled_codes.shape[0]
+    out_type = OUT_F16 if out_dtype == torch.float16 else OUT_F32
+    y = y if y is not None else _empty((m, n), out_dtype, x_half)
+    st = load().qi_hip_w4a16_gemm_tiled(_ptr(x_half), _ptr(w_tiled_codes), _ptr(w_tiled_scales), _ptr(bias),
+                                        _ptr(y), out_type, EPILOGUE_GELU_TANH if gelu else EPILOGUE_NONE, m, n, k,
+                                        _stream())
+    check(st, "w4a16 gemm")
+    return y
+
+
+def w4a16_gemv(x_half, w_tiled_codes, w_tiled_scales, bias=None, out_dtype=torch.float32, gelu=False, y=None):
+    m, k = x_half.shape
+    n = w_tiled_codes.shape[0]
+    out_type = OUT_F16 if out_dtype == torch.float16 else OUT_F32
+    y = y if y is not None else _empty((m, n), out_dtype, x_half)
+    st = load().qi_hip_w4a16_gemv(_ptr(x_half), _ptr(w_tiled_codes), _ptr(w_tiled_scales), _ptr(bias), _ptr(y),
+                                  out_type, EPILOGUE_GELU_TANH if gelu else EPILOGUE_NONE, m, n, k, _stream())
+    check(st, "w4a16 gemv")
+    return y

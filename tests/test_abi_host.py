@@ -1,0 +1,82 @@
+"""CPU tests of the boundary: the C-ABI library loads, exports every symbol
+the header declares, and rejects bad shapes before touching the GPU (the
+reference returns cudaErrorInvalidValue the same way, gemm.cu:185,264)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+import qwen_image_hip
+from qwen_image_hip import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "qwen_image_hip.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*int\s+(qi_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_reference_entry_points():
+    names = declared_functions()
+    for ref in ("qi_w4a4_quantize_activations", "qi_w4a4_gemm", "qi_w4a16_gemm", "qi_f32_to_f16"):
+        assert ref in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(declared_functions()) == set(_lib.SIGNATURES), "ctypes table out of sync with the header"
+
+
+def test_abi_version():
+    assert qwen_image_hip.load().qi_hip_abi_version() == _lib.ABI_VERSION
+
+
+INVALID = 1  # hipErrorInvalidValue
+
+
+@pytest.mark.parametrize("m,n,k", [(100, 128, 256), (128, 100, 256), (128, 128, 320), (129, 128, 256)])
+def test_reference_w4a4_shape_rules(m, n, k):
+    assert qwen_image_hip.load().qi_w4a4_gemm(8, 8, 8, 8, 8, m, n, k) == INVALID
+
+
+@pytest.mark.parametrize("m,n,k", [(100, 128, 64), (128, 100, 64), (128, 128, 96)])
+def test_reference_w4a16_shape_rules(m, n, k):
+    assert qwen_image_hip.load().qi_w4a16_gemm(8, 8, 8, 8, 8, m, n, k) == INVALID
+
+
+def test_extension_argument_checks():
+    L = qwen_image_hip.load()
+    assert L.qi_w4a4_quantize_activations(16, 16, 16, 4, 300) == INVALID          # k % 256
+    assert L.qi_hip_w4a4_quantize_activations_f16(16, 16, 16, 4, 255, None) == INVALID
+    assert L.qi_hip_w4a4_gemm_tiled(8, 8, 8, 8, None, 8, 0, 0, 5, 24, 256, None) == INVALID  # n % 16
+    assert L.qi_hip_w4a4_gemm_tiled(8, 8, 8, 8, None, 8, 2, 0, 5, 32, 256, None) == INVALID  # out type
+    assert L.qi_hip_w4a16_gemm_tiled(16, 8, 8, None, 8, 0, 7, 5, 32, 64, None) == INVALID    # epilogue
+    assert L.qi_hip_w4a16_gemv(16, 8, 8, None, 8, 0, 0, 17, 32, 64, None) == INVALID         # m > 16
+    assert L.qi_hip_w4a16_gemv(16, 8, 8, None, 8, 0, 0, 0, 32, 64, None) == INVALID
+    assert L.qi_hip_pack_weights(8, 8, 8, 8, 16, 320, 6, 0, None) == INVALID                 # k % 256
+    assert L.qi_hip_pack_weights(8, 8, 8, None, 16, 256, 5, 0, None) == INVALID             # no minimums
+    assert L.qi_hip_pack_weights(8, 8, 8, 8, 16, 256, 4, 0, None) == INVALID                 # scheme
+    assert L.qi_hip_relayout_w4a4(8, 8, 8, 8, 24, 256, None) == INVALID
+    assert L.qi_hip_relayout_w4a16(8, 8, 8, 8, 8, 16, 96, None) == INVALID
+    # misaligned operand pointers are refused, not faulted on
+    assert L.qi_hip_w4a4_gemm_tiled(9, 8, 8, 8, None, 8, 0, 0, 5, 32, 256, None) == INVALID
+    assert L.qi_w4a4_quantize_activations(18, 16, 16, 4, 256) == INVALID
+    # null pointers
+    assert L.qi_w4a4_gemm(None, None, None, None, None, 128, 128, 256) == INVALID
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch):
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "absent.so")
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(ImportError):
+        _lib.load()
+
+
+def test_error_wording_mirrors_reference():
+    e = _lib.QiHipError("w4a4 gemm", 1)
+    assert "w4a4 gemm failed" in str(e) and e.status == 1

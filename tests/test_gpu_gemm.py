@@ -1,0 +1,197 @@
+"""GPU parity: W4A4 GEMM, W4A16 GEMM, W4A16 GEMV, fused epilogues, linear().
+
+Bars (north star): int32 per-group partials bit-exact; W4A4 fp32 outputs are
+bit-exact with the oracle's reference-order fp32 formula (the kernel keeps
+that order); W4A16 / GEMV fp32 outputs within rel-L2 <= 1e-3 and
+max-abs <= 2e-2 * rms(out) of the float64 oracle; fp16 outputs are the same
+value rounded once more, so they get the same tolerance.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _data import (MAX_ABS_RMS_TOL, REL_L2_TOL, f16_bits, heavy_tailed, max_abs_over_rms, normal_f32, rel_l2,
+                   weights_f16)
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _h(bits, dev):
+    return _dev(np.ascontiguousarray(bits).view(np.float16), dev)
+
+
+def _close(got, want):
+    assert rel_l2(got, want) <= REL_L2_TOL, rel_l2(got, want)
+    assert max_abs_over_rms(got, want) <= MAX_ABS_RMS_TOL, max_abs_over_rms(got, want)
+
+
+def _w4a4_case(m, n, k, seed):
+    x = heavy_tailed(m, k, seed)
+    w = weights_f16(n, k, seed + 1)
+    a_codes, a_scales = oracle.quantize_activations(x)
+    w_codes, w_scales, _ = oracle.quantize_matrix(w, 6, clip=True)
+    return a_codes, a_scales, w_codes, w_scales
+
+
+# ------------------------------------------------------------------- W4A4 --
+
+@pytest.mark.parametrize("m,n,k", [(128, 128, 256), (256, 384, 768), (128, 256, 3072)])
+def test_w4a4_reference_abi_bit_exact(dev, m, n, k):
+    print(f"w4a4 reference abi m={m} n={n} k={k}", flush=True)
+    import qwen_image_hip.ops as ops
+    ac, as_, wc, ws = _w4a4_case(m, n, k, 100 + k)
+    want = oracle.w4a4_gemm(ac, as_, wc, ws)
+    got = ops.w4a4_gemm_reference(_dev(ac, dev), _h(as_, dev), _dev(wc, dev), _h(ws, dev)).cpu().numpy()
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    want64 = oracle.w4a4_gemm(ac, as_, wc, ws, f64=True)
+    _close(got, want64)
+
+
+def test_w4a4_reference_abi_rejects_shapes(dev):
+    import qwen_image_hip as q
+    lib = q.load()
+    assert lib.qi_w4a4_gemm(1, 1, 1, 1, 1, 100, 128, 256) == 1
+    assert lib.qi_w4a4_gemm(1, 1, 1, 1, 1, 128, 100, 256) == 1
+    assert lib.qi_w4a4_gemm(1, 1, 1, 1, 1, 128, 128, 320) == 1
+    assert lib.qi_w4a16_gemm(1, 1, 1, 1, 1, 128, 128, 96) == 1
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 16, 256), (5, 48, 512), (100, 256, 768), (263, 128, 1024),
+                                   (640, 1024, 512)])
+def test_w4a4_tiled_bit_exact(dev, m, n, k):
+    print(f"w4a4 tiled m={m} n={n} k={k}", flush=True)
+    import qwen_image_hip.ops as ops
+    ac, as_, wc, ws = _w4a4_case(m, n, k, 200 + m)
+    tc, ts = ops.relayout_w4a4(_dev(wc, dev), _h(ws, dev))
+    got = ops.w4a4_gemm(_dev(ac, dev), _h(as_, dev), tc, ts).cpu().numpy()
+    want = oracle.w4a4_gemm(ac, as_, wc, ws)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_w4a4_group_partials_exact(dev):
+    """Expose each int32 group partial: scales 1 on group g, 0 elsewhere."""
+    import qwen_image_hip.ops as ops
+    m, n, k = 64, 64, 512
+    ac, _, wc, _ = _w4a4_case(m, n, k, 300)
+    # Saturated codes too: every nibble -7 or 7 in the first rows.
+    ac[:2] = 0x77
+    ac[2:4] = 0x99
+    wc[:4] = 0x77
+    partials = oracle.w4a4_partials(ac, wc)          # [m, n, G]
+    assert np.abs(partials).max() == 64 * 49          # the int32 range is reached
+    tc_src = _dev(wc, dev)
+    G = k // 64
+    one = np.uint16(0x3C00)
+    for g in range(G):
+        sa = np.zeros((m, G), np.uint16)
+        sw = np.zeros((n, G), np.uint16)
+        sa[:, g] = one
+        sw[:, g] = one
+        tc, ts = ops.relayout_w4a4(tc_src, _h(sw, dev))
+        got = ops.w4a4_gemm(_dev(ac, dev), _h(sa, dev), tc, ts).cpu().numpy()
+        np.testing.assert_array_equal(got, partials[:, :, g].astype(np.float32))
+
+
+@pytest.mark.parametrize("gelu", [False, True])
+def test_w4a4_epilogue_f16_bias_gelu(dev, gelu):
+    import qwen_image_hip.ops as ops
+    m, n, k = 96, 128, 768
+    ac, as_, wc, ws = _w4a4_case(m, n, k, 400)
+    bias = np.random.default_rng(401).normal(0, 0.5, size=n).astype(np.float32)
+    tc, ts = ops.relayout_w4a4(_dev(wc, dev), _h(ws, dev))
+    got = ops.w4a4_gemm(_dev(ac, dev), _h(as_, dev), tc, ts, bias=_dev(bias, dev), out_dtype=torch.float16,
+                        gelu=gelu).float().cpu().numpy()
+    v = oracle.w4a4_gemm(ac, as_, wc, ws) + bias[None, :]
+    if gelu:
+        v = oracle.gelu_tanh(v)
+    want = oracle.half_to_f32(oracle.half_from_f32(v))
+    _close(got, want)
+
+
+# ------------------------------------------------------------------ W4A16 --
+
+def _w4a16_case(m, n, k, seed, clip=False):
+    xb = f16_bits(normal_f32(m, k, seed))
+    w = weights_f16(n, k, seed + 1)
+    codes, scales, mins = oracle.quantize_matrix(w, 5, clip=clip)
+    return xb, codes, scales, mins
+
+
+@pytest.mark.parametrize("m,n,k", [(128, 128, 64), (256, 256, 640), (128, 384, 3072)])
+def test_w4a16_reference_abi(dev, m, n, k):
+    print(f"w4a16 reference abi m={m} n={n} k={k}", flush=True)
+    import qwen_image_hip.ops as ops
+    xb, c, s, mn = _w4a16_case(m, n, k, 500 + k)
+    got = ops.w4a16_gemm_reference(_h(xb, dev), _dev(c, dev), _h(s, dev), _h(mn, dev)).cpu().numpy()
+    want = oracle.w4a16_gemm(xb, c, s, mn, precise=True)
+    _close(got, want)
+
+
+@pytest.mark.parametrize("m,n,k,clip", [(17, 16, 64, False), (100, 48, 192, True), (300, 512, 3584 // 64 * 64, False),
+                                        (1024, 256, 1024, True)])
+def test_w4a16_tiled(dev, m, n, k, clip):
+    print(f"w4a16 tiled m={m} n={n} k={k}", flush=True)
+    import qwen_image_hip.ops as ops
+    xb, c, s, mn = _w4a16_case(m, n, k, 600 + m, clip)
+    tc, ts = ops.relayout_w4a16(_dev(c, dev), _h(s, dev), _h(mn, dev))
+    got = ops.w4a16_gemm(_h(xb, dev), tc, ts).cpu().numpy()
+    want = oracle.w4a16_gemm(xb, c, s, mn, precise=True)
+    _close(got, want)
+
+
+@pytest.mark.parametrize("gelu", [False, True])
+def test_w4a16_epilogue_f16_bias_gelu(dev, gelu):
+    import qwen_image_hip.ops as ops
+    m, n, k = 160, 128, 512
+    xb, c, s, mn = _w4a16_case(m, n, k, 700)
+    bias = np.random.default_rng(701).normal(0, 0.5, size=n).astype(np.float32)
+    tc, ts = ops.relayout_w4a16(_dev(c, dev), _h(s, dev), _h(mn, dev))
+    got = ops.w4a16_gemm(_h(xb, dev), tc, ts, bias=_dev(bias, dev), out_dtype=torch.float16,
+                         gelu=gelu).float().cpu().numpy()
+    v = oracle.w4a16_gemm(xb, c, s, mn, precise=True) + bias[None, :]
+    if gelu:
+        v = oracle.gelu_tanh(v)
+    _close(got, oracle.half_to_f32(oracle.half_from_f32(v)))
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 18432, 3072), (2, 18432, 3072), (3, 64, 256), (16, 512, 3584 // 64 * 64)])
+def test_w4a16_gemv(dev, m, n, k):
+    print(f"gemv m={m} n={n} k={k}", flush=True)
+    import qwen_image_hip.ops as ops
+    xb, c, s, mn = _w4a16_case(m, n, k, 800 + m)
+    tc, ts = ops.relayout_w4a16(_dev(c, dev), _h(s, dev), _h(mn, dev))
+    got = ops.w4a16_gemv(_h(xb, dev), tc, ts).cpu().numpy()
+    want = oracle.w4a16_gemm(xb, c, s, mn, precise=True)
+    _close(got, want)
+    # The tiled GEMM entry point dispatches m <= 16 to the same kernel.
+    got2 = ops.w4a16_gemm(_h(xb, dev), tc, ts).cpu().numpy()
+    np.testing.assert_array_equal(got, got2)
+
+
+# ---------------------------------------------------------------- linear() --
+
+def test_linear_dispatch_and_reuse(dev):
+    """transformer.cplus:669-713 call pattern: Q quantises, K and V reuse it."""
+    import qwen_image_hip as q
+    rows, k, n = 136, 512, 256
+    x = heavy_tailed(rows, k, 900)
+    ws = [weights_f16(n, k, 901 + i) for i in range(3)]
+    work = q.Work(rows_max=256, k_max=1024, device=dev)
+    recs = [q.PackedLinear.from_fp16(q.SCHEME_W4A4_H256, _h(w, dev), clip=True) for w in ws]
+    xd = _dev(x, dev)
+    outs = [q.linear(recs[0], work, xd)]
+    outs += [q.linear(r, work, xd, reuse_input=True) for r in recs[1:]]
+    ac, as_ = oracle.quantize_activations(x)
+    for w, o in zip(ws, outs):
+        wc, wsc, _ = oracle.quantize_matrix(w, 6, clip=True)
+        np.testing.assert_array_equal(o.cpu().numpy(), oracle.w4a4_gemm(ac, as_, wc, wsc))
+
+    rec16 = q.PackedLinear.from_fp16(q.SCHEME_W4A16, _h(ws[0], dev))
+    y16 = q.linear(rec16, work, xd).cpu().numpy()
+    c, s, mn = oracle.quantize_matrix(ws[0], 5)
+    _close(y16, oracle.w4a16_gemm(oracle.half_from_f32(x), c, s, mn))
