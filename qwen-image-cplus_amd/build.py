@@ -33,6 +33,9 @@ HIP_FLAGS = [
     "-Wall",
     # Packed fp32 VALU forms stay off for all device code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results land in ordinary VGPRs, so the fp32 epilogues read them
+    # without an accumulator-register copy per element.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 

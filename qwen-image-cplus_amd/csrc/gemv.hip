@@ -49,8 +49,8 @@ __global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_kernel(
             for (int j = 0; j < 4; ++j) {
                 const float e0 = static_cast<float>((word >> (8 * j)) & 0xFu);
                 const float e1 = static_cast<float>((word >> (8 * j + 4)) & 0xFu);
-                w[half * 8 + 2 * j] = h2f(f2h(__builtin_fmaf(e0, s, mn)));
-                w[half * 8 + 2 * j + 1] = h2f(f2h(__builtin_fmaf(e1, s, mn)));
+                w[half * 8 + 2 * j] = h2f(dequant_w4a16(e0, s, mn));
+                w[half * 8 + 2 * j + 1] = h2f(dequant_w4a16(e1, s, mn));
             }
         }
 #pragma unroll

@@ -36,6 +36,20 @@ __device__ __forceinline__ uint16_t f2h(float v) {
     return __builtin_bit_cast(uint16_t, h);
 }
 
+// Pins a value to an fp32 register.  The backend otherwise folds
+// fp16(fmaf(a, b, c)) into one mixed-precision fma with a single rounding,
+// while the reference rounds to fp32 first and then to fp16.
+__device__ __forceinline__ float f32_round_point(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// fp16(fmaf(code, scale, minimum)) with the reference's two roundings
+// (qwen_image_cuda/cuda/gemm.cu:229-230).
+__device__ __forceinline__ uint16_t dequant_w4a16(float code, float scale, float minimum) {
+    return f2h(f32_round_point(__builtin_fmaf(code, scale, minimum)));
+}
+
 // ops.cu:156-160 (gelu_tanh_kernel) formula, evaluated in fp32.
 __device__ __forceinline__ float gelu_tanh(float v) {
     return 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));

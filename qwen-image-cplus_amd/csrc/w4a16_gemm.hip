@@ -29,8 +29,8 @@ __device__ __forceinline__ uint4 dequant8(uint32_t x, float scale, float minimum
     for (int j = 0; j < 4; ++j) {
         const float e0 = static_cast<float>((lo >> (8 * j)) & 0xFFu);
         const float e1 = static_cast<float>((hi >> (8 * j)) & 0xFFu);
-        out[j] = static_cast<uint32_t>(f2h(__builtin_fmaf(e0, scale, minimum))) |
-                 (static_cast<uint32_t>(f2h(__builtin_fmaf(e1, scale, minimum))) << 16);
+        out[j] = static_cast<uint32_t>(dequant_w4a16(e0, scale, minimum)) |
+                 (static_cast<uint32_t>(dequant_w4a16(e1, scale, minimum)) << 16);
     }
     return uint4{out[0], out[1], out[2], out[3]};
 }

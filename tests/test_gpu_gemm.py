@@ -195,3 +195,55 @@ def test_linear_dispatch_and_reuse(dev):
     y16 = q.linear(rec16, work, xd).cpu().numpy()
     c, s, mn = oracle.quantize_matrix(ws[0], 5)
     _close(y16, oracle.w4a16_gemm(oracle.half_from_f32(x), c, s, mn))
+
+
+# ------------------------------------------------- dequantisation exactness --
+
+def _double_rounding_cases(count, seed=0):
+    """(scale, minimum) fp16 pairs for which fp16(fmaf(c, s, m)) (the
+    reference's two roundings, gemm.cu:229-230) differs from a single rounding
+    of c*s + m for some code c, with every code's weight finite."""
+    g = np.random.default_rng(seed)
+    n = 2_000_000
+    s = g.integers(1, 0x7C00, n).astype(np.uint16)
+    m = g.integers(0, 0x10000, n).astype(np.uint16)
+    ok = (m & 0x7C00) != 0x7C00
+    s, m = s[ok], m[ok]
+    sf = s.view(np.float16).astype(np.float64)
+    mf = m.view(np.float16).astype(np.float64)
+    codes = np.arange(16, dtype=np.float64)[:, None]
+    exact = codes * sf[None, :] + mf[None, :]
+    with np.errstate(over="ignore"):
+        single = exact.astype(np.float16)
+        double = exact.astype(np.float32).astype(np.float16)
+    finite = np.all(np.isfinite(double), axis=0) & np.all(np.isfinite(single), axis=0)
+    differs = np.any(single.view(np.uint16) != double.view(np.uint16), axis=0)
+    idx = np.nonzero(finite & differs)[0][:count]
+    return s[idx], m[idx]
+
+
+@pytest.mark.parametrize("path", ["tiled", "reference", "gemv"])
+def test_w4a16_dequant_bit_exact_identity(dev, path):
+    """x = identity makes y = W^T exactly (one nonzero product per output), so
+    the kernels' dequantised weights are compared bit for bit with the oracle,
+    on (scale, minimum) pairs where double and single rounding disagree."""
+    import qwen_image_hip.ops as ops
+    n, k = 128, 128
+    s_adv, m_adv = _double_rounding_cases(n * 2)
+    assert len(s_adv) == n * 2
+    scales = s_adv.reshape(n, 2)
+    mins = m_adv.reshape(n, 2)
+    codes = np.random.default_rng(3).integers(0, 256, size=(n, k // 2), dtype=np.uint8)
+    want = oracle.w4a16_dequantize(codes, scales, mins).view(np.float16).astype(np.float32)   # [n, k]
+    eye = np.eye(k, dtype=np.float16)
+    if path == "reference":
+        got = ops.w4a16_gemm_reference(_dev(eye, dev), _dev(codes, dev), _h(scales, dev), _h(mins, dev))
+        got = got.cpu().numpy().T
+    else:
+        tc, ts = ops.relayout_w4a16(_dev(codes, dev), _h(scales, dev), _h(mins, dev))
+        if path == "tiled":
+            got = ops.w4a16_gemm(_dev(eye, dev), tc, ts).cpu().numpy().T
+        else:
+            got = np.concatenate([ops.w4a16_gemv(_dev(eye[r:r + 16], dev), tc, ts).cpu().numpy()
+                                  for r in range(0, k, 16)], axis=0).T
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
