@@ -9,6 +9,7 @@
 #define QI_API extern "C" __attribute__((visibility("default")))
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
@@ -73,6 +74,39 @@ __device__ __forceinline__ float wave_sum16(float v) {
 // place.  A 16*q operand on both MFMA sides yields 256*P exactly.
 __device__ __forceinline__ int nib_lo16(uint32_t x) { return static_cast<int>((x << 4) & 0xF0F0F0F0u); }
 __device__ __forceinline__ int nib_hi16(uint32_t x) { return static_cast<int>(x & 0xF0F0F0F0u); }
+
+// Buffer resource over [p, p + bytes): loads past the end return zeros, which
+// is how partial tiles read their missing rows.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), static_cast<short>(0), static_cast<int>(bytes),
+                                             0x00020000);
+}
+
+// 16 bytes per lane from a buffer straight into LDS (buffer_load ... lds):
+// lane i's bytes land at lds + 16 * i, so one wave instruction fills 1 KiB of
+// LDS contiguously starting at the wave-uniform `lds`.
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, void *lds, uint32_t voffset,
+                                                  uint32_t soffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)lds, 16, voffset,
+                                             soffset, 0, 0);
+}
+
+// Workgroup order that keeps the tiles resident on one XCD close together:
+// the hardware deals workgroups round-robin over the 8 XCDs, so consecutive
+// ids are remapped to one XCD's contiguous range, and tiles are walked in
+// bands of `band` tile-rows so an XCD's tiles share A rows and B columns in
+// its own L2.
+__device__ __forceinline__ void tile_of_block(int block, int tiles_m, int tiles_n, int band, int &tm, int &tn) {
+    const int total = tiles_m * tiles_n;
+    int b = block;
+    if (total % 8 == 0) b = (block % 8) * (total / 8) + block / 8;
+    const int per_band = band * tiles_n;
+    const int first_m = (b / per_band) * band;
+    const int rows = min(tiles_m - first_m, band);
+    const int in_band = b % per_band;
+    tm = first_m + in_band % rows;
+    tn = in_band / rows;
+}
 
 // Epilogue store of one fp32 value.
 __device__ __forceinline__ void store_out(void *y, size_t index, float v, int out_type) {
