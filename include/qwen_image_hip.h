@@ -24,12 +24,14 @@
  *                      lane l carries row 16*t + (l % 16), bytes
  *                      [8*(l/16), 8*(l/16) + 8) of that row's 32-byte group.
  *   W4A4 tiled scales  [N/16][G][16] fp16
- *   W4A16 tiled codes  [N/16][G][64 lanes][8 bytes]
- *                      lane l carries row 16*t + (l % 16), bytes
- *                      [4q, 4q+4) and [16+4q, 16+4q+4), q = l / 16.
+ *   W4A16 tiled codes  [N/16][G][64 lanes][2 dwords]
+ *                      lane l carries row 16*t + (l % 16), elements
+ *                      [8q, 8q+8) and [32+8q, 32+8q+8) of the group,
+ *                      q = l / 16, one dword each; within a dword element
+ *                      2i sits in nibble i and element 2i+1 in nibble 4+i.
  *   W4A16 tiled scales [N/16][G][16][2] fp16 pairs (scale, minimum)
  *
- * The byte contents are unchanged (a permutation); the *_inverse functions
+ * The re-layout is a permutation of nibbles and scales; the *_inverse functions
  * restore the QIPACK arrays exactly.  A tiled buffer has the same byte size
  * as the source arrays (scales and minimums are interleaved into one array of
  * twice the size for W4A16).

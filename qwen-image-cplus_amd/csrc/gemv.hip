@@ -2,8 +2,9 @@
 // whose cost is reading the int4 weights once from HBM.
 //
 // Arithmetic: W = fp16(fmaf(code, scale, minimum)) exactly as the W4A16 GEMM
-// (qwen_image_cuda/cuda/gemm.cu:222-230), products with the fp16 activations
-// accumulated in fp32.  The reference runs these linears in BF16 through
+// (qwen_image_cuda/cuda/gemm.cu:222-230), computed two weights per packed
+// fp16 instruction where that is provably the same value; weight x activation
+// pairs accumulate in fp32 with v_dot2 (exact fp16 products).  The reference runs these linears in BF16 through
 // cuBLAS SGEMM (qwen_image_cuda/src/transformer.cplus:716-730); there is no
 // INT4 GEMV there to follow.
 //
@@ -39,32 +40,22 @@ __global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_kernel(
     for (int r = 0; r < MR; ++r) acc[r] = 0.0f;
 
     auto consume = [&](int g, uint2 c, uint32_t sm) {
-        const float s = h2f(static_cast<uint16_t>(sm & 0xFFFFu));
-        const float mn = h2f(static_cast<uint16_t>(sm >> 16));
-        float w[16];
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const uint32_t word = half ? c.y : c.x;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float e0 = static_cast<float>((word >> (8 * j)) & 0xFu);
-                const float e1 = static_cast<float>((word >> (8 * j + 4)) & 0xFu);
-                w[half * 8 + 2 * j] = h2f(dequant_w4a16(e0, s, mn));
-                w[half * 8 + 2 * j + 1] = h2f(dequant_w4a16(e1, s, mn));
-            }
-        }
+        const uint32_t sb = sm & 0xFFFFu, mb = sm >> 16;
+        const bool fast = w4a16_single_rounding_exact(sb, mb);
+        const uint4 w0 = w4a16_dequant8(c.x, sb, mb, fast);   // elements [8q, 8q+8)
+        const uint4 w1 = w4a16_dequant8(c.y, sb, mb, fast);   // elements [32+8q, 32+8q+8)
+        const uint32_t ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
         for (int r = 0; r < MR; ++r) {
             if (r < m) {
-            const uint16_t *xr = x + static_cast<size_t>(r) * k + g * 64 + 8 * q;
-            const uint4 x0 = *reinterpret_cast<const uint4 *>(xr);
-            const uint4 x1 = *reinterpret_cast<const uint4 *>(xr + 32);
-            const uint32_t xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                const uint16_t *xr = x + static_cast<size_t>(r) * k + g * 64 + 8 * q;
+                const uint4 x0 = *reinterpret_cast<const uint4 *>(xr);
+                const uint4 x1 = *reinterpret_cast<const uint4 *>(xr + 32);
+                const uint32_t xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                acc[r] = __builtin_fmaf(w[2 * e], h2f(static_cast<uint16_t>(xs[e] & 0xFFFFu)), acc[r]);
-                acc[r] = __builtin_fmaf(w[2 * e + 1], h2f(static_cast<uint16_t>(xs[e] >> 16)), acc[r]);
-            }
+                for (int e = 0; e < 8; ++e)
+                    acc[r] = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2h, ws[e]), __builtin_bit_cast(v2h, xs[e]),
+                                                    acc[r], false);
             }
         }
     };

@@ -51,6 +51,62 @@ __device__ __forceinline__ uint16_t dequant_w4a16(float code, float scale, float
     return f2h(f32_round_point(__builtin_fmaf(code, scale, minimum)));
 }
 
+// W4A16 tiled codes hold a lane's 8 elements per dword with element 2i in
+// nibble slot i and element 2i+1 in slot 4+i, so (x >> 4i) & 0x000F000F is
+// the fp16-lane pair (e[2i], e[2i+1]) of small integers.
+__device__ __forceinline__ uint32_t w4a16_permute_nibbles(uint32_t x) {
+    uint32_t out = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out |= ((x >> (4 * e)) & 15u) << (4 * ((e & 1) ? 4 + (e >> 1) : (e >> 1)));
+    return out;
+}
+__device__ __forceinline__ uint32_t w4a16_unpermute_nibbles(uint32_t x) {
+    uint32_t out = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out |= ((x >> (4 * ((e & 1) ? 4 + (e >> 1) : (e >> 1)))) & 15u) << (4 * e);
+    return out;
+}
+
+// True when every c * scale + minimum (c = 0..15) is exactly representable in
+// fp32, so that one fp16 rounding of it equals the reference's two roundings.
+// c * scale has at most 15 significant bits and minimum 11; their exact sum
+// fits 24 bits when the exponent fields satisfy -12 <= es - em <= 8
+// (subnormals count as exponent field 1), or when minimum is zero.
+__device__ __forceinline__ bool w4a16_single_rounding_exact(uint32_t scale_bits, uint32_t minimum_bits) {
+    if ((minimum_bits & 0x7FFFu) == 0) return true;
+    const int es = max(static_cast<int>((scale_bits >> 10) & 31u), 1);
+    const int em = max(static_cast<int>((minimum_bits >> 10) & 31u), 1);
+    const int d = es - em;
+    return d <= 8 && d >= -12;
+}
+
+// 8 tiled (slot-permuted) codes -> 8 fp16 weights in element order.  Fast
+// path: packed fp16 integer trick and one fused fp16 fma per pair; exact
+// path: fp32 fma then RNE to fp16, per element (the reference's rounding).
+__device__ __forceinline__ uint4 w4a16_dequant8(uint32_t x, uint32_t scale_bits, uint32_t minimum_bits, bool fast) {
+    uint32_t out[4];
+    if (fast) {
+        const v2h s2 = __builtin_bit_cast(v2h, scale_bits | (scale_bits << 16));
+        const v2h m2 = __builtin_bit_cast(v2h, minimum_bits | (minimum_bits << 16));
+        const v2h k1024 = v2h{static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const v2h c = __builtin_bit_cast(v2h, ((x >> (4 * i)) & 0x000F000Fu) | 0x64006400u) - k1024;
+            out[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, s2, m2));
+        }
+    } else {
+        const float s = h2f(static_cast<uint16_t>(scale_bits)), mn = h2f(static_cast<uint16_t>(minimum_bits));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float e0 = static_cast<float>((x >> (4 * i)) & 15u);
+            const float e1 = static_cast<float>((x >> (4 * i + 16)) & 15u);
+            out[i] = static_cast<uint32_t>(dequant_w4a16(e0, s, mn)) |
+                     (static_cast<uint32_t>(dequant_w4a16(e1, s, mn)) << 16);
+        }
+    }
+    return uint4{out[0], out[1], out[2], out[3]};
+}
+
 // ops.cu:156-160 (gelu_tanh_kernel) formula, evaluated in fp32.
 __device__ __forceinline__ float gelu_tanh(float v) {
     return 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));

@@ -50,12 +50,17 @@ __global__ void relayout_w4a16_codes(const uint8_t *__restrict__ src, uint8_t *_
         const long long s0 = row * (k / 2) + g * 32 + 4 * q;  // k in [8q, 8q+8)
         const long long s1 = s0 + 16;                         // k in [32+8q, 32+8q+8)
         const long long d = i * 8;
+        // Within each dword the nibbles are also permuted (w4a16_permute_nibbles)
+        // so the kernels unpack element pairs with one shift-and-mask.
         if (inverse) {
-            *reinterpret_cast<uint32_t *>(dst + s0) = *reinterpret_cast<const uint32_t *>(src + d);
-            *reinterpret_cast<uint32_t *>(dst + s1) = *reinterpret_cast<const uint32_t *>(src + d + 4);
+            *reinterpret_cast<uint32_t *>(dst + s0) =
+                w4a16_unpermute_nibbles(*reinterpret_cast<const uint32_t *>(src + d));
+            *reinterpret_cast<uint32_t *>(dst + s1) =
+                w4a16_unpermute_nibbles(*reinterpret_cast<const uint32_t *>(src + d + 4));
         } else {
-            *reinterpret_cast<uint32_t *>(dst + d) = *reinterpret_cast<const uint32_t *>(src + s0);
-            *reinterpret_cast<uint32_t *>(dst + d + 4) = *reinterpret_cast<const uint32_t *>(src + s1);
+            *reinterpret_cast<uint32_t *>(dst + d) = w4a16_permute_nibbles(*reinterpret_cast<const uint32_t *>(src + s0));
+            *reinterpret_cast<uint32_t *>(dst + d + 4) =
+                w4a16_permute_nibbles(*reinterpret_cast<const uint32_t *>(src + s1));
         }
     }
 }

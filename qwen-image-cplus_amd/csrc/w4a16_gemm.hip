@@ -165,6 +165,195 @@ __global__ __launch_bounds__(WM *WAVE) void w4a16_gemm_kernel(
         }
 }
 
+// ---------------------------------------------------------------------------
+// Tiled-weight kernel.
+//
+// Roles.  The MFMA's A operand is the dequantised weight tile (16 outputs n)
+// and its B operand the activation tile (16 rows m), so the accumulator holds
+// y^T: each lane owns four consecutive outputs n of one row m and stores them
+// with one 8-byte (fp16) or 16-byte (fp32) write.
+//
+// Work split.  The NW wavefronts of a workgroup share the same BM activation
+// rows and own disjoint 16*TN-column slices of the weights, so every weight is
+// dequantised exactly once per workgroup, in registers, by the wave that uses
+// it, and only the activations need LDS.
+//
+// Latency.  Activation tiles (fp16 [BM][64] per 64-group) go memory -> LDS
+// with buffer_load ... lds into a ring of NSTAGE slots, and weight codes and
+// scales into a register ring, issued NSTAGE-1 groups ahead: at the MI355X's
+// memory latency a single group of MFMA work is far too short to cover a
+// load.  One barrier per group.  The eight 16-byte chunks of each activation
+// row are XOR-swizzled by (row & 7) so fragment reads spread over the banks.
+//
+// Dequantisation uses packed fp16 (two weights per instruction) when that is
+// provably the reference's value for the group's (scale, minimum), and the
+// reference's fp32 fma + RNE otherwise.
+template <int TM, int TN, int NW>
+__global__ __launch_bounds__(NW *WAVE, 2) void w4a16_tiled_kernel(
+    const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
+    const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int m, int n, int k) {
+    constexpr int NSTAGE = 4;
+    constexpr int BM = TM * 16, BN = NW * TN * 16;
+    constexpr int A_INSTR = BM / 8;  // 1 KiB = 8 rows x 128 bytes per direct load
+    static_assert(A_INSTR % NW == 0, "loader mapping");
+    constexpr int A_PER_W = A_INSTR / NW;
+    constexpr int LOADS_PER_GROUP = A_PER_W + 2 * TN;  // per wave
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_a[NSTAGE][BM][128];
+
+    const int groups = k >> 6;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
+    const int q = lane >> 4, r16 = lane & 15;
+    const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
+    int tm, tn;
+    tile_of_block(blockIdx.x, tiles_m, tiles_n, 8, tm, tn);
+    const int block_row = tm * BM, block_col = tn * BN;
+
+    const uint32_t x_bytes = static_cast<uint32_t>(m) * static_cast<uint32_t>(k) * 2u;
+    const uint32_t c_bytes = static_cast<uint32_t>(n) * static_cast<uint32_t>(k / 2);
+    const uint32_t s_bytes = static_cast<uint32_t>(n) * static_cast<uint32_t>(groups) * 4u;
+    const auto rx = buffer_rsrc(x, x_bytes);
+    const auto rc = buffer_rsrc(codes, c_bytes);
+    const auto rs = buffer_rsrc(scales, s_bytes);
+
+    // Activation direct loads: instruction I covers rows 8I..8I+7; lane L
+    // fills LDS chunk L % 8 of row 8I + L / 8 with global chunk
+    // (L % 8) ^ (row & 7).
+    uint32_t x_vo[A_PER_W];
+#pragma unroll
+    for (int u = 0; u < A_PER_W; ++u) {
+        const int I = wave * A_PER_W + u;
+        const int row = 8 * I + (lane >> 3), grow = block_row + row;
+        const int chunk = (lane & 7) ^ (row & 7);
+        x_vo[u] = grow < m ? static_cast<uint32_t>(grow) * k * 2u + chunk * 16u : x_bytes;
+    }
+    // This wave's weight tiles.
+    uint32_t c_vo[TN], s_vo[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int tile = block_col / 16 + wave * TN + j;
+        const bool ok = tile < n / 16;
+        c_vo[j] = ok ? static_cast<uint32_t>(tile) * groups * 512u + lane * 8u : c_bytes;
+        s_vo[j] = ok ? static_cast<uint32_t>(tile) * groups * 64u + r16 * 4u : s_bytes;
+    }
+
+    v2i c_ring[NSTAGE][TN];
+    uint32_t s_ring[NSTAGE][TN];
+    auto issue = [&](int g, int slot) {
+#pragma unroll
+        for (int u = 0; u < A_PER_W; ++u) {
+            const int I = wave * A_PER_W + u;
+            buffer_load_lds16(rx, &lds_a[slot][8 * I][0], x_vo[u], g * 128);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            c_ring[slot][j] = __builtin_amdgcn_raw_buffer_load_b64(rc, c_vo[j], g * 512, 0);
+            s_ring[slot][j] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, s_vo[j], g * 64, 0));
+        }
+    };
+
+    v4f acc[TN][TM];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int i = 0; i < TM; ++i) acc[j][i] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int slot) {
+        // Dequantise this wave's weight fragments for both K-steps.
+        v8h wf[2][TN];
+        bool fast = true;
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+            fast = fast && w4a16_single_rounding_exact(s_ring[slot][j] & 0xFFFFu, s_ring[slot][j] >> 16);
+        // One wave-uniform choice: the packed path unless some lane's group
+        // needs the fp32 path.
+        fast = __all(fast);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const uint32_t sb = s_ring[slot][j] & 0xFFFFu, mb = s_ring[slot][j] >> 16;
+            wf[0][j] = __builtin_bit_cast(v8h, w4a16_dequant8(static_cast<uint32_t>(c_ring[slot][j][0]), sb, mb, fast));
+            wf[1][j] = __builtin_bit_cast(v8h, w4a16_dequant8(static_cast<uint32_t>(c_ring[slot][j][1]), sb, mb, fast));
+        }
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            // All of this step's activation fragments first (TM LDS reads in
+            // flight), then the TM x TN MFMAs.
+            v8h xf[TM];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int row = 16 * i + r16;
+                const int chunk = (4 * st + q) ^ (row & 7);
+                xf[i] = *reinterpret_cast<const v8h *>(&lds_a[slot][row][chunk * 16]);
+            }
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[st][j], xf[i], acc[j][i], 0, 0, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, TM, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
+        }
+    };
+
+    // Prologue: groups 0 .. NSTAGE-2 in flight.  Loads are issued
+    // unconditionally, also past the last group: those read harmless bytes
+    // (the next tile or row, or zeros past the end) into slots that are never
+    // consumed, and keep the number of loads in flight per group constant.
+#pragma unroll
+    for (int p = 0; p < NSTAGE - 1; ++p) issue(p, p);
+
+    // Main loop, unrolled by the ring length so ring indices are constants.
+    for (int g0 = 0; g0 < groups; g0 += NSTAGE) {
+#pragma unroll
+        for (int u = 0; u < NSTAGE; ++u) {
+            const int g = g0 + u;
+            // Group g's loads are complete once at most the (NSTAGE - 2)
+            // later groups' loads remain in flight.
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTAGE - 2) * LOADS_PER_GROUP) : "memory");
+            __syncthreads();
+            issue(g + NSTAGE - 1, (u + NSTAGE - 1) % NSTAGE);
+            if (g < groups) compute(u);
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // acc[j][i][r] = y[row, col]: row = m-tile i, lane r16; col = this wave's
+    // n-tile j, 4q + r.
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int col = block_col + (wave * TN + j) * 16 + 4 * q;
+        if (col >= n) continue;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int row = block_row + 16 * i + r16;
+            if (row >= m) continue;
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = epilogue(acc[j][i][r], bias, col + r, epi);
+            const size_t idx = static_cast<size_t>(row) * n + col;
+            if (out_type == QI_HIP_OUT_F16) {
+                uint2 h;
+                h.x = static_cast<uint32_t>(f2h(v[0])) | (static_cast<uint32_t>(f2h(v[1])) << 16);
+                h.y = static_cast<uint32_t>(f2h(v[2])) | (static_cast<uint32_t>(f2h(v[3])) << 16);
+                *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(y) + idx) = h;
+            } else {
+                *reinterpret_cast<float4 *>(reinterpret_cast<float *>(y) + idx) = float4{v[0], v[1], v[2], v[3]};
+            }
+        }
+    }
+}
+
+template <int TM, int TN, int NW>
+static int launch_tiled(const void *x, const void *codes, const void *scales, const float *bias, void *y,
+                        int out_type, int epi, int m, int n, int k, hipStream_t stream) {
+    constexpr int BM = TM * 16, BN = NW * TN * 16;
+    const long long blocks = static_cast<long long>((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+    if (blocks > 0x7FFFFFFFLL) return kInvalid;
+    w4a16_tiled_kernel<TM, TN, NW><<<dim3(static_cast<unsigned>(blocks)), dim3(NW * WAVE), 0, stream>>>(
+        static_cast<const uint16_t *>(x), static_cast<const uint8_t *>(codes), static_cast<const uint16_t *>(scales),
+        bias, y, out_type, epi, m, n, k);
+    return launch_status();
+}
+
 template <int TM, int TN, int WM, bool TILED>
 static int launch(const void *x, const void *codes, const void *scales, const void *minimums, const float *bias,
                   void *y, int out_type, int epi, int m, int n, int k, hipStream_t stream) {
@@ -217,6 +406,18 @@ QI_API int qi_hip_w4a16_gemm_tiled(const void *x_half, const void *w_tiled_codes
     if (m <= 16)
         return qi_hip_w4a16_gemv_impl(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
                                       stream_of(stream));
-    const uint16_t *ts = static_cast<const uint16_t *>(w_tiled_scales);
-    return dispatch<true>(x_half, w_tiled_codes, ts, ts + 1, bias, y, out_type, epilogue, m, n, k, stream_of(stream));
+    if (static_cast<long long>(m) * k * 2 >= (1LL << 32) || static_cast<long long>(n) * (k / 2) >= (1LL << 32))
+        return kInvalid;
+    // Small m: short row tiles so the grid still covers the 256 CUs.
+    if (m <= 256)
+        return launch_tiled<2, 1, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
+                                     stream_of(stream));
+    if (m <= 1024)
+        return launch_tiled<4, 1, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
+                                     stream_of(stream));
+    if (n % 192 == 0)
+        return launch_tiled<8, 3, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
+                                     stream_of(stream));
+    return launch_tiled<8, 2, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
+                                 stream_of(stream));
 }

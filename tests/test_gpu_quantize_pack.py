@@ -113,10 +113,20 @@ def _expected_w4a4_tiles(codes, scales):
     return c, s
 
 
+def _permute_nibbles(words):
+    # element 2i -> nibble i, element 2i+1 -> nibble 4+i, within each dword
+    out = np.zeros_like(words)
+    for e in range(8):
+        slot = 4 + e // 2 if e % 2 else e // 2
+        out |= ((words >> np.uint32(4 * e)) & np.uint32(15)) << np.uint32(4 * slot)
+    return out
+
+
 def _expected_w4a16_tiles(codes, scales, mins):
     n, hk = codes.shape
     G = hk * 2 // 64
     c = codes.reshape(n // 16, 16, G, 2, 4, 4).transpose(0, 2, 4, 1, 3, 5).reshape(n, hk)
+    c = _permute_nibbles(np.ascontiguousarray(c).view(np.uint32)).view(np.uint8).reshape(n, hk)
     sm = np.stack([scales, mins], axis=-1).reshape(n // 16, 16, G, 2).transpose(0, 2, 1, 3).reshape(n, 2 * G)
     return c, sm
 
