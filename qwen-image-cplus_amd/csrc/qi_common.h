@@ -131,6 +131,17 @@ __device__ __forceinline__ float wave_sum16(float v) {
 __device__ __forceinline__ int nib_lo16(uint32_t x) { return static_cast<int>((x << 4) & 0xF0F0F0F0u); }
 __device__ __forceinline__ int nib_hi16(uint32_t x) { return static_cast<int>(x & 0xF0F0F0F0u); }
 
+// Signed int4 code (-7..7) -> fp6 E2M3 bits (sign, 2 exponent bits with bias
+// 1, 3 mantissa bits).  Every integer in [-7, 7] is exact in E2M3, so MFMAs
+// on these operands accumulate the exact integer dot product.
+__device__ __forceinline__ uint32_t int4_to_e2m3(int q) {
+    // |q| 0..7 -> magnitude codes 0, 8 (1.0), 16 (2.0), 20 (3.0), 24 (4.0),
+    // 26 (5.0), 28 (6.0), 30 (7.0).
+    const uint32_t a = static_cast<uint32_t>(q < 0 ? -q : q);
+    const uint32_t code = a == 0 ? 0u : (a == 1 ? 8u : (a < 4 ? 16u + 4u * (a - 2) : 24u + 2u * (a - 4)));
+    return (q < 0 ? 32u : 0u) | code;
+}
+
 // Buffer resource over [p, p + bytes): loads past the end return zeros, which
 // is how partial tiles read their missing rows.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uint32_t bytes) {

@@ -48,9 +48,14 @@ __device__ __forceinline__ void load4<uint16_t>(const uint16_t *src, float v[4])
     v[3] = h2f(static_cast<uint16_t>(t.y >> 16));
 }
 
-template <typename In>
+// FMT 0: QIPACK activation layout (codes [m, k/2] nibbles, scales [m, k/64]).
+// FMT 1: fp6 MFMA-operand layout: codes [m/16][G][64 lanes][12 bytes] where
+//        lane q*16 + (row % 16) holds the E2M3 codes of inputs 16q..16q+15 of
+//        the group, 6 bits each, little-endian; scales [m/16][G][16] fp16.
+template <typename In, int FMT>
 __global__ __launch_bounds__(QUANT_WAVES * WAVE) void quantize_chunks_kernel(
-    const In *__restrict__ x, uint8_t *__restrict__ codes, uint16_t *__restrict__ scales, long long chunks) {
+    const In *__restrict__ x, uint8_t *__restrict__ codes, uint16_t *__restrict__ scales, long long chunks,
+    int chunks_per_row) {
     __shared__ float lds[QUANT_WAVES][256];
     const int lane = threadIdx.x & (WAVE - 1);
     const int wave = threadIdx.x >> 6;
@@ -99,10 +104,27 @@ __global__ __launch_bounds__(QUANT_WAVES * WAVE) void quantize_chunks_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) c[j] = static_cast<int>(fminf(fmaxf(rintf(v[j] / scale), -7.0f), 7.0f));
     if (active) {
-        const uint16_t packed = static_cast<uint16_t>((c[0] & 0xF) | ((c[1] & 0xF) << 4) | ((c[2] & 0xF) << 8) |
-                                                      ((c[3] & 0xF) << 12));
-        reinterpret_cast<uint16_t *>(codes)[chunk * 64 + lane] = packed;
-        if ((lane & 15) == 0) scales[chunk * 4 + (lane >> 4)] = scale_bits;
+        if (FMT == 0) {
+            const uint16_t packed = static_cast<uint16_t>((c[0] & 0xF) | ((c[1] & 0xF) << 4) | ((c[2] & 0xF) << 8) |
+                                                          ((c[3] & 0xF) << 12));
+            reinterpret_cast<uint16_t *>(codes)[chunk * 64 + lane] = packed;
+            if ((lane & 15) == 0) scales[chunk * 4 + (lane >> 4)] = scale_bits;
+        } else {
+            // This lane's four inputs are 4p..4p+3 of slice q of group g: 24
+            // bits at byte 3p of the 12-byte operand slot.
+            const long long row = chunk / chunks_per_row;
+            const int groups = chunks_per_row * 4;
+            const int g = static_cast<int>(chunk % chunks_per_row) * 4 + (lane >> 4);
+            const int q = (lane & 15) >> 2, p = lane & 3;
+            const uint32_t bits = int4_to_e2m3(c[0]) | (int4_to_e2m3(c[1]) << 6) | (int4_to_e2m3(c[2]) << 12) |
+                                  (int4_to_e2m3(c[3]) << 18);
+            const long long block = (row >> 4) * groups + g;
+            uint8_t *dst = codes + block * 768 + (q * 16 + (row & 15)) * 12 + 3 * p;
+            dst[0] = static_cast<uint8_t>(bits);
+            dst[1] = static_cast<uint8_t>(bits >> 8);
+            dst[2] = static_cast<uint8_t>(bits >> 16);
+            if ((lane & 15) == 0) scales[block * 16 + (row & 15)] = scale_bits;
+        }
     }
 }
 
@@ -124,7 +146,7 @@ __global__ void f32_to_f16_kernel(const float *__restrict__ src, uint16_t *__res
     }
 }
 
-template <typename In>
+template <typename In, int FMT>
 static int launch_quantize(const In *x, void *codes, void *scales, int m, int k, hipStream_t stream) {
     if (m < 0 || k <= 0 || k % 256 != 0 || (m > 0 && (!x || !codes || !scales))) return kInvalid;
     if (m == 0) return 0;
@@ -135,8 +157,8 @@ static int launch_quantize(const In *x, void *codes, void *scales, int m, int k,
     const long long chunks = static_cast<long long>(m) * (k / 256);
     const long long blocks = (chunks + QUANT_WAVES - 1) / QUANT_WAVES;
     if (blocks > 0x7FFFFFFFLL) return kInvalid;
-    quantize_chunks_kernel<In><<<dim3(static_cast<unsigned>(blocks)), dim3(QUANT_WAVES * WAVE), 0, stream>>>(
-        x, static_cast<uint8_t *>(codes), static_cast<uint16_t *>(scales), chunks);
+    quantize_chunks_kernel<In, FMT><<<dim3(static_cast<unsigned>(blocks)), dim3(QUANT_WAVES * WAVE), 0, stream>>>(
+        x, static_cast<uint8_t *>(codes), static_cast<uint16_t *>(scales), chunks, k / 256);
     return launch_status();
 }
 
@@ -156,17 +178,26 @@ static int launch_f32_to_f16(const float *src, void *out, unsigned long long cou
 QI_API int qi_hip_abi_version(void) { return QI_HIP_ABI_VERSION; }
 
 QI_API int qi_w4a4_quantize_activations(const float *x, void *codes, void *scales, int m, int k) {
-    return qi::launch_quantize<float>(x, codes, scales, m, k, nullptr);
+    return qi::launch_quantize<float, 0>(x, codes, scales, m, k, nullptr);
 }
 
 QI_API int qi_hip_w4a4_quantize_activations(const float *x, void *codes, void *scales, int m, int k,
                                             void *stream) {
-    return qi::launch_quantize<float>(x, codes, scales, m, k, qi::stream_of(stream));
+    return qi::launch_quantize<float, 0>(x, codes, scales, m, k, qi::stream_of(stream));
 }
 
 QI_API int qi_hip_w4a4_quantize_activations_f16(const void *x_half, void *codes, void *scales, int m, int k,
                                                 void *stream) {
-    return qi::launch_quantize<uint16_t>(static_cast<const uint16_t *>(x_half), codes, scales, m, k,
+    return qi::launch_quantize<uint16_t, 0>(static_cast<const uint16_t *>(x_half), codes, scales, m, k,
+                                            qi::stream_of(stream));
+}
+
+QI_API int qi_hip_w4a4_quantize_activations_fp6(const void *x, int x_is_half, void *codes6, void *scales_tiled, int m,
+                                                int k, void *stream) {
+    if (x_is_half)
+        return qi::launch_quantize<uint16_t, 1>(static_cast<const uint16_t *>(x), codes6, scales_tiled, m, k,
+                                                qi::stream_of(stream));
+    return qi::launch_quantize<float, 1>(static_cast<const float *>(x), codes6, scales_tiled, m, k,
                                          qi::stream_of(stream));
 }
 

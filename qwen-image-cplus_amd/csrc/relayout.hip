@@ -90,6 +90,36 @@ __global__ void relayout_scales(const uint16_t *__restrict__ scales, const uint1
     }
 }
 
+// W4A4 weights as fp6 MFMA operands: [N/16][G][64 lanes][12 bytes], lane
+// q*16 + r holding the E2M3 codes of inputs 16q..16q+15 of row 16t + r.
+__global__ void relayout_w4a4_fp6_codes(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int n, int k) {
+    const int groups = k / GROUP;
+    const long long total = static_cast<long long>(n / 16) * groups * WAVE;
+    for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += static_cast<long long>(gridDim.x) * blockDim.x) {
+        const int lane = static_cast<int>(i % WAVE);
+        const long long tg = i / WAVE;
+        const int g = static_cast<int>(tg % groups);
+        const long long t = tg / groups;
+        const long long row = t * 16 + (lane & 15);
+        const uint2 w = *reinterpret_cast<const uint2 *>(src + row * (k / 2) + g * 32 + 8 * (lane >> 4));
+        uint32_t out[3] = {0u, 0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const uint32_t word = e < 8 ? w.x : w.y;
+            const int nib = static_cast<int>((word >> (4 * (e & 7))) & 15u);
+            const uint32_t v = int4_to_e2m3(nib >= 8 ? nib - 16 : nib);
+            const int bit = 6 * e;
+            out[bit >> 5] |= v << (bit & 31);
+            if ((bit & 31) > 26) out[(bit >> 5) + 1] |= v >> (32 - (bit & 31));
+        }
+        uint8_t *d = dst + i * 12;
+        *reinterpret_cast<uint32_t *>(d) = out[0];
+        *reinterpret_cast<uint32_t *>(d + 4) = out[1];
+        *reinterpret_cast<uint32_t *>(d + 8) = out[2];
+    }
+}
+
 static unsigned grid_for(long long work, int block) {
     long long b = (work + block - 1) / block;
     if (b > 65536LL * 8) b = 65536LL * 8;
@@ -164,5 +194,19 @@ QI_API int qi_hip_relayout_w4a16_inverse(const void *tiled_codes, const void *ti
     relayout_scales<<<grid_for(static_cast<long long>(n) * (k / GROUP), 256), 256, 0, s>>>(
         nullptr, nullptr, const_cast<uint16_t *>(static_cast<const uint16_t *>(tiled_scales)), n, k, 1,
         static_cast<uint16_t *>(scales), static_cast<uint16_t *>(minimums));
+    return launch_status();
+}
+
+QI_API int qi_hip_relayout_w4a4_fp6(const void *codes, const void *scales, void *codes6, void *tiled_scales, int n,
+                                    int k, void *stream) {
+    if (n <= 0 || k <= 0 || n % 16 || k % 256 || !codes || !scales || !codes6 || !tiled_scales) return kInvalid;
+    if (!aligned(codes, 8) || !aligned(codes6, 4) || !aligned(scales, 2) || !aligned(tiled_scales, 2)) return kInvalid;
+    hipStream_t s = stream_of(stream);
+    const long long lanes = static_cast<long long>(n / 16) * (k / GROUP) * WAVE;
+    relayout_w4a4_fp6_codes<<<grid_for(lanes, 256), 256, 0, s>>>(static_cast<const uint8_t *>(codes),
+                                                                  static_cast<uint8_t *>(codes6), n, k);
+    relayout_scales<<<grid_for(static_cast<long long>(n) * (k / GROUP), 256), 256, 0, s>>>(
+        static_cast<const uint16_t *>(scales), nullptr, static_cast<uint16_t *>(tiled_scales), n, k, 0, nullptr,
+        nullptr);
     return launch_status();
 }

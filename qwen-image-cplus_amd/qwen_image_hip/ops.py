@@ -187,3 +187,52 @@ def w4a16_gemv(x_half, w_tiled_codes, w_tiled_scales, bias=None, out_dtype=torch
                                   out_type, EPILOGUE_GELU_TANH if gelu else EPILOGUE_NONE, m, n, k, _stream())
     check(st, "w4a16 gemv")
     return y
+
+
+# ------------------------------------------------------------ fp6 W4A4 path --
+
+
+def fp6_rows(m: int) -> int:
+    """Rows an fp6 activation buffer holds for m rows (whole 16-row tiles)."""
+    return (m + 15) // 16 * 16
+
+
+def quantize_activations_fp6(x: torch.Tensor, codes6: torch.Tensor | None = None,
+                             scales: torch.Tensor | None = None):
+    """Quantise rows of x into the fp6 MFMA-operand layout.
+
+    Returns (codes6 uint8 [ceil(m/16)*16, 3k/4], scales fp16 [ceil(m/16)*16, k/64]) in
+    tile order (see qwen_image_hip.h).  Same codes as quantize_activations.
+    """
+    m, k = x.shape
+    rows = fp6_rows(m)
+    codes6 = codes6 if codes6 is not None else _empty((rows, k * 3 // 4), torch.uint8, x)
+    scales = scales if scales is not None else _empty((rows, k // GROUP), torch.float16, x)
+    if x.dtype not in (torch.float32, torch.float16):
+        raise TypeError("activations must be float32 or float16")
+    st = load().qi_hip_w4a4_quantize_activations_fp6(_ptr(x), 1 if x.dtype == torch.float16 else 0, _ptr(codes6),
+                                                     _ptr(scales), m, k, _stream())
+    check(st, "activation quantization")
+    return codes6, scales
+
+
+def relayout_w4a4_fp6(codes: torch.Tensor, scales: torch.Tensor):
+    n, half_k = codes.shape
+    k = half_k * 2
+    c6 = _empty((n, k * 3 // 4), torch.uint8, codes)
+    ts = torch.empty_like(scales)
+    check(load().qi_hip_relayout_w4a4_fp6(_ptr(codes), _ptr(scales), _ptr(c6), _ptr(ts), n, k, _stream()),
+          "relayout")
+    return c6, ts
+
+
+def w4a4_gemm_fp6(a_codes6, a_scales_tiled, w_codes6, w_scales_tiled, m: int, bias=None,
+                  out_dtype=torch.float32, gelu=False, y=None):
+    n, k = w_codes6.shape[0], w_codes6.shape[1] * 4 // 3
+    out_type = OUT_F16 if out_dtype == torch.float16 else OUT_F32
+    y = y if y is not None else _empty((m, n), out_dtype, w_codes6)
+    st = load().qi_hip_w4a4_gemm_fp6(_ptr(a_codes6), _ptr(a_scales_tiled), _ptr(w_codes6), _ptr(w_scales_tiled),
+                                     _ptr(bias), _ptr(y), out_type, EPILOGUE_GELU_TANH if gelu else EPILOGUE_NONE,
+                                     m, n, k, _stream())
+    check(st, "w4a4 gemm")
+    return y

@@ -1,0 +1,123 @@
+"""GPU parity of the fp6-operand W4A4 path: quantiser codes, weight re-layout,
+and the GEMM (bit-exact with the oracle's reference-order fp32 formula, and
+exposing exact int32 group partials)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _data import heavy_tailed, weights_f16
+
+pytestmark = pytest.mark.gpu
+
+_MAG = {0: 0, 8: 1, 16: 2, 20: 3, 24: 4, 26: 5, 28: 6, 30: 7}
+
+
+def _dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _h(bits, dev):
+    return _dev(np.ascontiguousarray(bits).view(np.float16), dev)
+
+
+def _u16(t):
+    return t.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def decode_fp6_tiles(buf: np.ndarray, rows: int, k: int) -> np.ndarray:
+    """fp6 operand tiles [rows/16][G][64 lanes][12 B] -> int codes [rows, k]."""
+    G = k // 64
+    b = buf.reshape(rows // 16, G, 64, 12).astype(np.uint32)
+    b = np.concatenate([b, np.zeros(b.shape[:-1] + (1,), np.uint32)], axis=-1)
+    vals = np.zeros(b.shape[:-1] + (16,), np.int64)
+    lut = np.zeros(64, np.int64)
+    for code, mag in _MAG.items():
+        lut[code] = mag
+        lut[code | 32] = -mag
+    for j in range(16):
+        bit = 6 * j
+        byte, shift = bit // 8, bit % 8
+        word = b[..., byte] | (b[..., byte + 1] << 8)
+        vals[..., j] = lut[(word >> shift) & 63]
+    # [t, g, q, r, j] -> [t, r, g, q, j]
+    v = vals.reshape(rows // 16, G, 4, 16, 16).transpose(0, 3, 1, 2, 4)
+    return v.reshape(rows, k)
+
+
+def unpack_nibbles(codes: np.ndarray) -> np.ndarray:
+    v = np.stack([codes & 15, codes >> 4], -1).reshape(codes.shape[0], -1).astype(np.int64)
+    return np.where(v > 7, v - 16, v)
+
+
+def tiled_scales(scales: np.ndarray, rows: int) -> np.ndarray:
+    """[rows, G] -> [rows/16][G][16] as stored by the fp6 path."""
+    G = scales.shape[1]
+    return scales.reshape(rows // 16, 16, G).transpose(0, 2, 1).reshape(rows, G)
+
+
+@pytest.mark.parametrize("m,k,half", [(16, 256, False), (37, 768, True), (128, 3072, False)])
+def test_fp6_quantizer_matches_codes(dev, m, k, half):
+    import qwen_image_hip.ops as ops
+    x = heavy_tailed(m, k, 31 + m)
+    xin = x.astype(np.float16) if half else x
+    want_c, want_s = oracle.quantize_activations(xin.view(np.uint16) if half else xin)
+    c6, s6 = ops.quantize_activations_fp6(_dev(xin, dev))
+    rows = ops.fp6_rows(m)
+    codes = decode_fp6_tiles(c6.cpu().numpy(), rows, k)[:m]
+    np.testing.assert_array_equal(codes, unpack_nibbles(want_c))
+    pad = np.zeros((rows, k // 64), np.uint16)
+    pad[:m] = want_s
+    got_s = _u16(s6).reshape(rows, k // 64)
+    np.testing.assert_array_equal(tiled_scales(got_s, rows)[:m] if False else got_s.reshape(rows // 16, k // 64, 16)
+                                  .transpose(0, 2, 1).reshape(rows, k // 64)[:m], want_s)
+
+
+def test_fp6_weight_relayout(dev):
+    import qwen_image_hip.ops as ops
+    n, k = 48, 512
+    w = weights_f16(n, k, 41)
+    c, s, _ = oracle.quantize_matrix(w, 6, clip=True)
+    c6, ts = ops.relayout_w4a4_fp6(_dev(c, dev), _h(s, dev))
+    np.testing.assert_array_equal(decode_fp6_tiles(c6.cpu().numpy(), n, k), unpack_nibbles(c))
+    np.testing.assert_array_equal(_u16(ts).reshape(n, k // 64), tiled_scales(s, n))
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 16, 256), (5, 48, 512), (100, 256, 768), (263, 128, 1024),
+                                   (640, 1024, 512), (1024, 512, 3072)])
+def test_fp6_gemm_bit_exact(dev, m, n, k):
+    print(f"fp6 gemm m={m} n={n} k={k}", flush=True)
+    import qwen_image_hip.ops as ops
+    x = heavy_tailed(m, k, 500 + m)
+    w = weights_f16(n, k, 501 + n)
+    ac, as_ = oracle.quantize_activations(x)
+    wc, ws, _ = oracle.quantize_matrix(w, 6, clip=True)
+    a6, sa = ops.quantize_activations_fp6(_dev(x, dev))
+    w6, sw = ops.relayout_w4a4_fp6(_dev(wc, dev), _h(ws, dev))
+    got = ops.w4a4_gemm_fp6(a6, sa, w6, sw, m).cpu().numpy()
+    want = oracle.w4a4_gemm(ac, as_, wc, ws)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_fp6_group_partials_exact(dev):
+    """Scales 1 on one group and 0 elsewhere expose each exact partial."""
+    import qwen_image_hip.ops as ops
+    m, n, k = 64, 64, 512
+    x = heavy_tailed(m, k, 600)
+    x[:2] = 1000.0                                   # saturated rows
+    w = weights_f16(n, k, 601)
+    ac, _ = oracle.quantize_activations(x)
+    wc, _, _ = oracle.quantize_matrix(w, 6)
+    wc[:4] = 0x77
+    partials = oracle.w4a4_partials(ac, wc)
+    a6, sa = ops.quantize_activations_fp6(_dev(x, dev))
+    G = k // 64
+    for g in range(G):
+        s_act = np.zeros((m, G), np.uint16)
+        s_w = np.zeros((n, G), np.uint16)
+        s_act[:, g] = 0x3C00
+        s_w[:, g] = 0x3C00
+        w6, sw = ops.relayout_w4a4_fp6(_dev(wc, dev), _h(s_w, dev))
+        sa_t = _h(tiled_scales(s_act, m), dev)
+        got = ops.w4a4_gemm_fp6(a6, sa_t, w6, sw, m).cpu().numpy()
+        np.testing.assert_array_equal(got, partials[:, :, g].astype(np.float32))
