@@ -7,10 +7,12 @@ GELU-tanh, down 12288->3072), W4A4 with H256/g64: every
 distinct input is quantised online (Q/K/V share one quantisation, as the
 reference's reuse_input does) and all seven GEMMs run.  value = block TOPS
 (2*M*N*K int ops per GEMM, quantiser work not counted).  The same pass with
-W4A16 weights (config 2) and the M=1/M=2 modulation GEMV (config 4) are
-reported beside it.
+W4A16 weights (config 2), the same W4A4 pass on the int8 operand path and
+the M=1/M=2 modulation GEMV (config 4) are reported beside it.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-extra]
+    python bench.py --kernel-only    # the dominant GEMM x 20 + a 512 MiB copy,
+                                     # the workload of the counter runs
 """
 from __future__ import annotations
 
@@ -52,7 +54,7 @@ def block_ops() -> float:
 class Block:
     """Random-init weights of one block (both streams), packed on the device."""
 
-    def __init__(self, scheme: int, seed: int):
+    def __init__(self, scheme: int, seed: int, operand: str = "fp6"):
         import torch
         import qwen_image_hip as q
 
@@ -64,7 +66,8 @@ class Block:
                 w = (torch.randn((n, k), generator=g, device="cuda") * 0.02).half()
                 # W4A4 packs use the clip search; W4A16 packs do not (the
                 # reference's published packs, README.md:38).
-                self.layers[(stream, name)] = q.PackedLinear.from_fp16(scheme, w, clip=(scheme == q.SCHEME_W4A4_H256))
+                self.layers[(stream, name)] = q.PackedLinear.from_fp16(
+                    scheme, w, clip=(scheme == q.SCHEME_W4A4_H256), operand=operand)
                 del w
         torch.cuda.synchronize()
 
@@ -82,47 +85,43 @@ def heavy_tailed(m, k, g):
 
 
 class StepW4A4:
+    """One block's W4A4 linears through the transformer::linear mirror: every
+    distinct input quantised once (K and V reuse Q's codes), MLP up with the
+    fused GELU, its fp16 output quantised again for MLP down."""
+
     def __init__(self, block: Block, seed: int):
         import torch
-        from qwen_image_hip import ops
+        import qwen_image_hip as q
 
-        self.ops = ops
+        self.q = q
         g = torch.Generator(device="cuda")
         g.manual_seed(seed)
         self.block = block
         self.bufs = {}
         for stream, m in STREAMS.items():
-            b = {
+            self.bufs[stream] = {
                 "x_qkv": heavy_tailed(m, HIDDEN, g), "x_out": heavy_tailed(m, HIDDEN, g),
                 "x_mlp": heavy_tailed(m, HIDDEN, g),
-                "codes": torch.empty((m, MLP // 2), dtype=torch.uint8, device="cuda"),
-                "scales": torch.empty((m, MLP // 64), dtype=torch.float16, device="cuda"),
+                "work": q.Work(m, MLP, "cuda"),
                 "y": torch.empty((m, HIDDEN), dtype=torch.float16, device="cuda"),
                 "h": torch.empty((m, MLP), dtype=torch.float16, device="cuda"),
             }
-            self.bufs[stream] = b
-
-    def codes(self, b, m, k):
-        return b["codes"].view(-1)[: m * k // 2].view(m, k // 2), b["scales"].view(-1)[: m * k // 64].view(m, k // 64)
 
     def __call__(self):
-        ops = self.ops
-        for stream, m in STREAMS.items():
+        import torch
+
+        lin = self.q.linear
+        f16 = torch.float16
+        for stream in STREAMS:
             b = self.bufs[stream]
             L = lambda name: self.block.layers[(stream, name)]  # noqa: E731
-            c, s = self.codes(b, m, HIDDEN)
-            ops.quantize_activations(b["x_qkv"], c, s)
-            for name in ("to_q", "to_k", "to_v"):
-                ops.w4a4_gemm(c, s, L(name).tiled_codes, L(name).tiled_scales, out_dtype=ops.torch.float16, y=b["y"])
-            ops.quantize_activations(b["x_out"], c, s)
-            ops.w4a4_gemm(c, s, L("to_out").tiled_codes, L("to_out").tiled_scales, out_dtype=ops.torch.float16, y=b["y"])
-            ops.quantize_activations(b["x_mlp"], c, s)
-            ops.w4a4_gemm(c, s, L("mlp_up").tiled_codes, L("mlp_up").tiled_scales, out_dtype=ops.torch.float16,
-                          gelu=True, y=b["h"])
-            c2, s2 = self.codes(b, m, MLP)
-            ops.quantize_activations(b["h"], c2, s2)
-            ops.w4a4_gemm(c2, s2, L("mlp_down").tiled_codes, L("mlp_down").tiled_scales, out_dtype=ops.torch.float16,
-                          y=b["y"])
+            w = b["work"]
+            lin(L("to_q"), w, b["x_qkv"], b["y"], out_dtype=f16)
+            lin(L("to_k"), w, b["x_qkv"], b["y"], reuse_input=True, out_dtype=f16)
+            lin(L("to_v"), w, b["x_qkv"], b["y"], reuse_input=True, out_dtype=f16)
+            lin(L("to_out"), w, b["x_out"], b["y"], out_dtype=f16)
+            lin(L("mlp_up"), w, b["x_mlp"], b["h"], out_dtype=f16, gelu=True)
+            lin(L("mlp_down"), w, b["h"], b["y"], out_dtype=f16)
 
 
 class StepW4A16:
@@ -173,19 +172,54 @@ def time_fn(fn, iters, warmup):
 
 
 def dominant_kernel(block: Block, step: StepW4A4):
-    """The image-stream to_q W4A4 GEMM (M=4096, N=K=3072) timed alone."""
-    from qwen_image_hip import ops
+    """The image-stream to_q W4A4 GEMM (M=4096, N=K=3072) timed alone, with
+    HIP events on the stream it is launched on."""
     import torch
 
     m = STREAMS["image"]
     b = step.bufs["image"]
-    c, s = step.codes(b, m, HIDDEN)
-    ops.quantize_activations(b["x_qkv"], c, s)
     L = block.layers[("image", "to_q")]
-    fn = lambda: ops.w4a4_gemm(c, s, L.tiled_codes, L.tiled_scales, out_dtype=torch.float16, y=b["y"])  # noqa: E731
+    lin = step.q.linear
+    lin(L, b["work"], b["x_qkv"], b["y"], out_dtype=torch.float16)
+    fn = lambda: lin(L, b["work"], b["x_qkv"], b["y"], reuse_input=True, out_dtype=torch.float16)  # noqa: E731
     ms = time_fn(fn, 50, 5)
     ops_per_launch = 2.0 * m * HIDDEN * HIDDEN
     return ms, ops_per_launch
+
+
+def kernel_only():
+    """Dominant W4A4 GEMM x 20, then a plain 512 MiB copy x 5 whose known byte
+    count calibrates the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+    import qwen_image_hip as q
+
+    m = STREAMS["image"]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1)
+    w = (torch.randn((HIDDEN, HIDDEN), generator=g, device="cuda") * 0.02).half()
+    rec = q.PackedLinear.from_fp16(q.SCHEME_W4A4_H256, w, clip=True)
+    work = q.Work(m, HIDDEN, "cuda")
+    x = heavy_tailed(m, HIDDEN, g)
+    y = torch.empty((m, HIDDEN), dtype=torch.float16, device="cuda")
+    q.linear(rec, work, x, y, out_dtype=torch.float16)
+    for _ in range(20):
+        q.linear(rec, work, x, y, reuse_input=True, out_dtype=torch.float16)
+    src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log("kernel-only: 20 x w4a4 GEMM 4096x3072x3072, 5 x copy 536870912 B")
+    return 0
+
+
+def time_block(operand: str, seed: int, steps: int, warmup: int):
+    """ms per W4A4 block step with the given operand format."""
+    import qwen_image_hip as q
+
+    blk = Block(q.SCHEME_W4A4_H256, seed, operand)
+    step = StepW4A4(blk, seed + 1)
+    return time_fn(step, steps, warmup)
 
 
 def bench_gemv(iters=200):
@@ -222,10 +256,12 @@ def bench_gemv(iters=200):
     return out
 
 
-def cpu_baseline(seconds_target=12.0):
+def cpu_baseline(budget_s=20.0):
     """The CPU oracle (C, OpenMP over the host cores) on a bounded sample of
-    the same workload: activation quantisation + W4A4 GEMM of the to_q shape
-    (N = K = 3072) over a slice of image-stream rows; TOPS = 2*M*N*K / time."""
+    the same workload: the block's W4A4 linears (quantise + GEMM per linear,
+    K/V reusing Q's codes) in step order, image stream first, stopping once
+    about budget_s seconds of CPU work have run.  TOPS = 2*M*N*K of the
+    GEMMs that ran / their time (weights packed outside the timed part)."""
     import numpy as np
 
     sys.path.insert(0, str(ROOT / "oracle"))
@@ -234,22 +270,29 @@ def cpu_baseline(seconds_target=12.0):
     from _data import heavy_tailed as ht, weights_f16
 
     oracle.lib()
-    w = weights_f16(HIDDEN, HIDDEN, 5)
-    wc, ws, _ = oracle.quantize_matrix(w, 6, clip=True)
-    rows = 16
-    while True:
-        x = ht(rows, HIDDEN, 6)
-        t0 = time.perf_counter()
-        ac, as_ = oracle.quantize_activations(x)
-        oracle.w4a4_gemm(ac, as_, wc, ws)
-        dt = time.perf_counter() - t0
-        if dt * 4 >= seconds_target or rows >= 4096:
-            break
-        rows = min(4096, rows * max(2, int(seconds_target / max(dt, 1e-3) / 4)))
-    ops_ = 2.0 * rows * HIDDEN * HIDDEN
-    return {"value": round(ops_ / dt / 1e12, 6), "unit": "TOPS", "cores": oracle.num_threads(), "kind": "port",
-            "sample": f"W4A4 quantise + GEMM, M={rows} of the image stream, N=K={HIDDEN} (to_q), "
-                      f"{dt:.2f} s on {os.cpu_count()} host CPUs ({platform.processor() or platform.machine()})"}
+    done_ops, spent, ran = 0.0, 0.0, []
+    seed = 10
+    for stream, m in STREAMS.items():
+        x_in = None
+        for name, n, k in block_shapes():
+            if spent >= budget_s:
+                break
+            seed += 1
+            wc, ws, _ = oracle.quantize_matrix(weights_f16(n, k, seed), 6, clip=True)
+            if name in ("to_q", "to_out", "mlp_up", "mlp_down"):
+                x_in = ht(m, k, seed + 100)
+            t0 = time.perf_counter()
+            if name not in ("to_k", "to_v"):
+                ac, as_ = oracle.quantize_activations(x_in)
+            oracle.w4a4_gemm(ac, as_, wc, ws)
+            spent += time.perf_counter() - t0
+            done_ops += 2.0 * m * n * k
+            ran.append(f"{stream}.{name}")
+    return {"value": round(done_ops / spent / 1e12, 6), "unit": "TOPS", "cores": oracle.num_threads(),
+            "kind": "port",
+            "sample": f"CPU oracle W4A4 quantise + GEMM over {len(ran)} of the block's 12 linears "
+                      f"({', '.join(ran)}), {done_ops / 1e9:.1f} G int-ops in {spent:.1f} s on "
+                      f"{oracle.num_threads()} threads ({platform.processor() or platform.machine()})"}
 
 
 def main(argv=None) -> int:
@@ -259,6 +302,9 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="only the headline W4A4 block")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="run only the dominant GEMM (20 launches) and a 512 MiB device copy (5 launches), "
+                         "for hardware-counter runs")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -270,7 +316,9 @@ def main(argv=None) -> int:
 
     q.load()
     torch.cuda.set_device(0)
-    log("packing W4A4 block weights")
+    if args.kernel_only:
+        return kernel_only()
+    log("packing W4A4 block weights (fp6 operands)")
     blk4 = Block(q.SCHEME_W4A4_H256, 1)
     step4 = StepW4A4(blk4, 2)
     for _ in range(args.warmup):
@@ -298,12 +346,17 @@ def main(argv=None) -> int:
             traffic = None
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_OPS / 1e12, "unit": "TFLOP/s",
                 "frac": round(achieved * 1e12 / PEAK_INT8_OPS, 4), "traffic": traffic,
-                "kernel": "w4a4_gemm_kernel M=4096 N=3072 K=3072 (int8 MFMA ops)", "ms_per_launch": round(dom_ms, 4)}
+                "kernel": "w4a4_fp6_kernel M=4096 N=3072 K=3072 (int ops vs dense int8 MFMA peak)",
+                "ms_per_launch": round(dom_ms, 4)}
     del step4, blk4
     torch.cuda.empty_cache()
 
     extra = {}
     if not args.no_extra:
+        log("W4A4 block on the int8 operand path")
+        ms8 = time_block("int8", 5, args.steps, args.warmup)
+        extra["w4a4_int8_block"] = {"ms_per_step": round(ms8, 4), "TOPS": round(block_ops() / (ms8 * 1e-3) / 1e12, 1)}
+        torch.cuda.empty_cache()
         log("packing W4A16 block weights")
         blk16 = Block(q.SCHEME_W4A16, 3)
         step16 = StepW4A16(blk16, 4)
@@ -327,7 +380,7 @@ def main(argv=None) -> int:
         "metric": "QIPACK W4A4/W4A16 linear TOPS + % roofline, MMDiT block @1024^2 (M=4352)",
         "value": round(tops, 2), "unit": "TOPS", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int4xint4->int32 (int8 MFMA), fp32 epilogue, fp16 out", "data": "synthetic",
+        "dtype": "int4 x int4 exact group partials (fp6 E2M3 MFMA operands), fp32 epilogue, fp16 out", "data": "synthetic",
         "config": {"workload": "W4A4 H256 g64 one MMDiT dual-stream block linears (config 3): image M=4096 + "
                                "text M=256, hidden 3072, MLP 12288, heavy-tailed fp16 activations, online quantiser",
                    "global_batch": 1, "seq_len": sum(STREAMS.values()), "parallelism": "single-gpu"},

@@ -8,5 +8,6 @@ host-side mirror of the reference's linear-op interface.
 """
 from ._lib import ABI_VERSION, LIB_PATH, QiHipError, load  # noqa: F401
 from . import ops  # noqa: F401
-from .linear import SCHEME_W4A16, SCHEME_W4A4_H256, PackedLinear, Work, linear  # noqa: F401
+from .linear import (SCHEME_W4A16, SCHEME_W4A4_H256, W4A4_FP6, W4A4_INT8, PackedLinear, Work,  # noqa: F401
+                     linear)
 from . import qipack  # noqa: F401

@@ -17,6 +17,14 @@ the activation scratch the reference sizes in ``allocate_work``
 (transformer.cplus:638-667).  Unlike the reference, rows need not be a
 multiple of 128, outputs may be fp16 with a fused bias/GELU epilogue, and
 m <= 16 dispatches to the bandwidth-bound GEMV.
+
+W4A4 records run on one of two operand formats, both bit-identical to the
+reference's arithmetic (gemm.cu:137-168):
+
+* ``W4A4_FP6`` (default): the int4 codes are widened once to 6-bit E2M3
+  floats in MFMA-operand tiles and multiplied on the f8f6f4 matrix core,
+  which returns the exact group partials already in fp32;
+* ``W4A4_INT8``: nibble tiles multiplied on the int8 matrix core.
 """
 from __future__ import annotations
 
@@ -28,6 +36,8 @@ from . import ops
 
 SCHEME_W4A16 = 5
 SCHEME_W4A4_H256 = 6
+W4A4_FP6 = "fp6"
+W4A4_INT8 = "int8"
 
 
 @dataclass
@@ -40,28 +50,35 @@ class PackedLinear:
     tiled_codes: torch.Tensor
     tiled_scales: torch.Tensor
     bias: torch.Tensor | None = None  # fp32 [n] or None (the reference has none)
+    operand: str = W4A4_FP6  # W4A4 records only
 
     @classmethod
     def from_qipack(cls, scheme: int, codes: torch.Tensor, scales: torch.Tensor,
-                    minimums: torch.Tensor | None = None, bias: torch.Tensor | None = None) -> "PackedLinear":
+                    minimums: torch.Tensor | None = None, bias: torch.Tensor | None = None,
+                    operand: str = W4A4_FP6) -> "PackedLinear":
         """Upload hook: re-lay the QIPACK arrays of one record (device tensors)."""
         n, half_k = codes.shape
         if scheme == SCHEME_W4A4_H256:
-            tc, ts = ops.relayout_w4a4(codes, scales)
+            if operand == W4A4_FP6:
+                tc, ts = ops.relayout_w4a4_fp6(codes, scales)
+            elif operand == W4A4_INT8:
+                tc, ts = ops.relayout_w4a4(codes, scales)
+            else:
+                raise ValueError(f"unknown W4A4 operand format {operand!r}")
         elif scheme == SCHEME_W4A16:
             if minimums is None:
                 raise ValueError("W4A16 records carry a minimums (zeros) array")
             tc, ts = ops.relayout_w4a16(codes, scales, minimums)
         else:
             raise ValueError(f"unsupported INT4 scheme {scheme}")
-        return cls(scheme, n, half_k * 2, tc, ts, bias)
+        return cls(scheme, n, half_k * 2, tc, ts, bias, operand)
 
     @classmethod
     def from_fp16(cls, scheme: int, w_half: torch.Tensor, clip: bool = False,
-                  bias: torch.Tensor | None = None) -> "PackedLinear":
+                  bias: torch.Tensor | None = None, operand: str = W4A4_FP6) -> "PackedLinear":
         """Quantise an fp16 [N, K] matrix with the QIPACK quantiser, then re-lay it."""
         codes, scales, mins = ops.pack_weights(w_half, scheme, clip)
-        return cls.from_qipack(scheme, codes, scales, mins, bias)
+        return cls.from_qipack(scheme, codes, scales, mins, bias, operand)
 
 
 class Work:
@@ -70,8 +87,11 @@ class Work:
     def __init__(self, rows_max: int, k_max: int, device: torch.device | str = "cuda"):
         self.rows_max = rows_max
         self.k_max = k_max
-        self.codes = torch.empty(rows_max * k_max // 2, dtype=torch.uint8, device=device)
-        self.code_scales = torch.empty(rows_max * k_max // ops.GROUP, dtype=torch.float16, device=device)
+        # Sized for the fp6 operand tiles (whole 16-row tiles, 3/4 byte per
+        # input), which also hold the nibble layout (1/2 byte per input).
+        rows16 = ops.fp6_rows(rows_max)
+        self.codes = torch.empty(rows16 * k_max * 3 // 4, dtype=torch.uint8, device=device)
+        self.code_scales = torch.empty(rows16 * k_max // ops.GROUP, dtype=torch.float16, device=device)
         self.halves = torch.empty(rows_max * k_max, dtype=torch.float16, device=device)
 
     def views(self, rows: int, k: int):
@@ -80,6 +100,13 @@ class Work:
         return (self.codes[: rows * k // 2].view(rows, k // 2),
                 self.code_scales[: rows * k // ops.GROUP].view(rows, k // ops.GROUP),
                 self.halves[: rows * k].view(rows, k))
+
+    def fp6_views(self, rows: int, k: int):
+        if rows > self.rows_max or k > self.k_max:
+            raise ValueError("work buffers are smaller than this linear")
+        r16 = ops.fp6_rows(rows)
+        return (self.codes[: r16 * k * 3 // 4].view(r16, k * 3 // 4),
+                self.code_scales[: r16 * k // ops.GROUP].view(r16, k // ops.GROUP))
 
 
 def linear(record: PackedLinear, work: Work, input: torch.Tensor, output: torch.Tensor | None = None,
@@ -96,6 +123,12 @@ def linear(record: PackedLinear, work: Work, input: torch.Tensor, output: torch.
     if input.shape[-1] != k:
         raise ValueError(f"input width {input.shape[-1]} != record inputs {k}")
     codes, code_scales, halves = work.views(rows, k)
+    if record.scheme == SCHEME_W4A4_H256 and record.operand == W4A4_FP6:
+        codes6, scales6 = work.fp6_views(rows, k)
+        if not reuse_input:
+            ops.quantize_activations_fp6(input[:rows], codes6, scales6)
+        return ops.w4a4_gemm_fp6(codes6, scales6, record.tiled_codes, record.tiled_scales, rows, record.bias,
+                                 out_dtype, gelu, output)
     if record.scheme == SCHEME_W4A4_H256:
         if not reuse_input:
             ops.quantize_activations(input[:rows], codes, code_scales)

@@ -175,14 +175,15 @@ def test_w4a16_gemv(dev, m, n, k):
 
 # ---------------------------------------------------------------- linear() --
 
-def test_linear_dispatch_and_reuse(dev):
+@pytest.mark.parametrize("operand", ["fp6", "int8"])
+def test_linear_dispatch_and_reuse(dev, operand):
     """transformer.cplus:669-713 call pattern: Q quantises, K and V reuse it."""
     import qwen_image_hip as q
     rows, k, n = 136, 512, 256
     x = heavy_tailed(rows, k, 900)
     ws = [weights_f16(n, k, 901 + i) for i in range(3)]
     work = q.Work(rows_max=256, k_max=1024, device=dev)
-    recs = [q.PackedLinear.from_fp16(q.SCHEME_W4A4_H256, _h(w, dev), clip=True) for w in ws]
+    recs = [q.PackedLinear.from_fp16(q.SCHEME_W4A4_H256, _h(w, dev), clip=True, operand=operand) for w in ws]
     xd = _dev(x, dev)
     outs = [q.linear(recs[0], work, xd)]
     outs += [q.linear(r, work, xd, reuse_input=True) for r in recs[1:]]
