@@ -131,25 +131,27 @@ int qi_hip_w4a16_gemv(const void *x_half, const void *w_tiled_codes, const void 
                       const float *bias, void *y, int out_type, int epilogue, int m, int n, int k, void *stream);
 
 /* fp6 operand path for W4A4.  The int4 codes -7..7 are exact in FP6 E2M3, so
- * the gfx950 f8f6f4 MFMA yields the same exact per-group integer partials as
- * the int8 MFMA, already in fp32.  Layout of both operands: per 16-row tile t
- * and 64-group g, 768 bytes = 64 lanes x 12 bytes; lane q*16 + r holds the
- * E2M3 codes of inputs 16q..16q+15 of row 16t + r, 6 bits each,
- * little-endian.  Scales per (t, g): 16 fp16, one per row.
+ * the gfx950 f8f6f4 MFMA (32x32x64: K = one g64 group) yields the same exact
+ * per-group integer partials as the int8 MFMA, already in fp32.  Layout of
+ * both operands: per 32-row tile T and 64-group g, 1536 bytes = 2 halves x
+ * 64 lanes x 12 bytes; lane l of half h holds the E2M3 codes (6 bits each,
+ * little-endian) of inputs 32*(l/32) + 16h .. + 15 of the group, row
+ * 32T + l%32.  Scales [rows/32][G][32] fp16 (tile, group, row).
  *
  * Quantiser (same arithmetic and codes as qi_w4a4_quantize_activations):
- * x is f32 (x_is_half = 0) or fp16 [m, k]; codes6 holds ceil(m/16) * 16 rows
- * (rows past m are left unwritten and never stored from); k % 256 == 0. */
+ * x is f32 (x_is_half = 0) or fp16 [m, k]; codes6 holds ceil(m/32) * 32 rows
+ * (rows past m are left unwritten and never stored from); k % 256 == 0;
+ * codes6 4-byte aligned. */
 int qi_hip_w4a4_quantize_activations_fp6(const void *x, int x_is_half, void *codes6, void *scales_tiled, int m,
                                          int k, void *stream);
 /* One-time re-layout of QIPACK W4A4 weights (codes [n, k/2], scales [n, G])
- * into the fp6 operand layout above (1 byte per weight) plus tiled scales
- * [n/16][G][16].  n % 16 == 0, k % 256 == 0. */
+ * into the fp6 operand layout above (3/4 byte per weight) plus tiled scales.
+ * n % 32 == 0, k % 256 == 0. */
 int qi_hip_relayout_w4a4_fp6(const void *codes, const void *scales, void *codes6, void *tiled_scales, int n, int k,
                              void *stream);
 /* W4A4 GEMM on the fp6 operands; same result, bit for bit, as
- * qi_hip_w4a4_gemm_tiled on the same codes.  Any m >= 1; n % 16 == 0;
- * k % 256 == 0. */
+ * qi_hip_w4a4_gemm_tiled on the same codes.  Any m >= 1; n % 32 == 0;
+ * k % 256 == 0; y aligned to 16 bytes (f32) or 8 bytes (f16). */
 int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *a_scales_tiled, const void *w_codes6,
                          const void *w_scales_tiled, const float *bias, void *y, int out_type, int epilogue, int m,
                          int n, int k, void *stream);

@@ -49,9 +49,10 @@ __device__ __forceinline__ void load4<uint16_t>(const uint16_t *src, float v[4])
 }
 
 // FMT 0: QIPACK activation layout (codes [m, k/2] nibbles, scales [m, k/64]).
-// FMT 1: fp6 MFMA-operand layout: codes [m/16][G][64 lanes][12 bytes] where
-//        lane q*16 + (row % 16) holds the E2M3 codes of inputs 16q..16q+15 of
-//        the group, 6 bits each, little-endian; scales [m/16][G][16] fp16.
+// FMT 1: fp6 MFMA-operand layout: per 32-row tile T and group g, 1536 bytes
+//        = 2 halves x 64 lanes x 12 bytes; lane l of half h holds the E2M3
+//        codes (6 bits each, little-endian) of inputs 32 * (l / 32) + 16h ..
+//        + 15 of the group, row 32T + l % 32.  Scales [m/32][G][32] fp16.
 template <typename In, int FMT>
 __global__ __launch_bounds__(QUANT_WAVES * WAVE) void quantize_chunks_kernel(
     const In *__restrict__ x, uint8_t *__restrict__ codes, uint16_t *__restrict__ scales, long long chunks,
@@ -110,20 +111,27 @@ __global__ __launch_bounds__(QUANT_WAVES * WAVE) void quantize_chunks_kernel(
             reinterpret_cast<uint16_t *>(codes)[chunk * 64 + lane] = packed;
             if ((lane & 15) == 0) scales[chunk * 4 + (lane >> 4)] = scale_bits;
         } else {
-            // This lane's four inputs are 4p..4p+3 of slice q of group g: 24
-            // bits at byte 3p of the 12-byte operand slot.
+            // This lane's four inputs are 4p..4p+3 of slice q of group g
+            // (inputs 16q..16q+15).  Slice q goes to half q & 1 of the
+            // (32-row tile, group) block, lane slot 32 * (q >> 1) + row % 32,
+            // whose 12 bytes are the 24-bit runs of lanes p = 0..3: lane p
+            // < 3 assembles and stores dword p.
             const long long row = chunk / chunks_per_row;
             const int groups = chunks_per_row * 4;
             const int g = static_cast<int>(chunk % chunks_per_row) * 4 + (lane >> 4);
             const int q = (lane & 15) >> 2, p = lane & 3;
             const uint32_t bits = int4_to_e2m3(c[0]) | (int4_to_e2m3(c[1]) << 6) | (int4_to_e2m3(c[2]) << 12) |
                                   (int4_to_e2m3(c[3]) << 18);
-            const long long block = (row >> 4) * groups + g;
-            uint8_t *dst = codes + block * 768 + (q * 16 + (row & 15)) * 12 + 3 * p;
-            dst[0] = static_cast<uint8_t>(bits);
-            dst[1] = static_cast<uint8_t>(bits >> 8);
-            dst[2] = static_cast<uint8_t>(bits >> 16);
-            if ((lane & 15) == 0) scales[block * 16 + (row & 15)] = scale_bits;
+            const uint32_t next = static_cast<uint32_t>(__shfl_down(static_cast<int>(bits), 1, 64));
+            const long long block = (row >> 5) * groups + g;
+            const int r32 = static_cast<int>(row & 31);
+            if (p < 3) {
+                const uint32_t word = (bits >> (8 * p)) | (next << (24 - 8 * p));
+                uint32_t *dst = reinterpret_cast<uint32_t *>(codes + block * 1536 + (q & 1) * 768 +
+                                                             ((q >> 1) * 32 + r32) * 12);
+                dst[p] = word;
+            }
+            if ((lane & 15) == 0) scales[block * 32 + r32] = scale_bits;
         }
     }
 }
@@ -150,8 +158,9 @@ template <typename In, int FMT>
 static int launch_quantize(const In *x, void *codes, void *scales, int m, int k, hipStream_t stream) {
     if (m < 0 || k <= 0 || k % 256 != 0 || (m > 0 && (!x || !codes || !scales))) return kInvalid;
     if (m == 0) return 0;
-    // Vector loads: 4 elements per lane; 2-byte code stores.
-    if (reinterpret_cast<uintptr_t>(x) % (4 * sizeof(In)) != 0 || reinterpret_cast<uintptr_t>(codes) % 2 != 0 ||
+    // Vector loads: 4 elements per lane; 2-byte (QIPACK) or 4-byte (fp6) code stores.
+    if (reinterpret_cast<uintptr_t>(x) % (4 * sizeof(In)) != 0 ||
+        reinterpret_cast<uintptr_t>(codes) % (FMT == 0 ? 2 : 4) != 0 ||
         reinterpret_cast<uintptr_t>(scales) % 2 != 0)
         return kInvalid;
     const long long chunks = static_cast<long long>(m) * (k / 256);

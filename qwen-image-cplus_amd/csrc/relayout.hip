@@ -90,19 +90,23 @@ __global__ void relayout_scales(const uint16_t *__restrict__ scales, const uint1
     }
 }
 
-// W4A4 weights as fp6 MFMA operands: [N/16][G][64 lanes][12 bytes], lane
-// q*16 + r holding the E2M3 codes of inputs 16q..16q+15 of row 16t + r.
+// W4A4 weights as fp6 MFMA operands, the layout the activation quantiser
+// writes: per 32-row tile T and group g, 2 halves x 64 lanes x 12 bytes; lane
+// l of half h holds the E2M3 codes of inputs 32 * (l / 32) + 16h .. + 15 of
+// row 32T + l % 32.  One thread per 12-byte lane slot.
 __global__ void relayout_w4a4_fp6_codes(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int n, int k) {
     const int groups = k / GROUP;
-    const long long total = static_cast<long long>(n / 16) * groups * WAVE;
+    const long long total = static_cast<long long>(n / 32) * groups * 2 * WAVE;
     for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
          i += static_cast<long long>(gridDim.x) * blockDim.x) {
         const int lane = static_cast<int>(i % WAVE);
-        const long long tg = i / WAVE;
+        const int half = static_cast<int>((i / WAVE) & 1);
+        const long long tg = i / (2 * WAVE);
         const int g = static_cast<int>(tg % groups);
         const long long t = tg / groups;
-        const long long row = t * 16 + (lane & 15);
-        const uint2 w = *reinterpret_cast<const uint2 *>(src + row * (k / 2) + g * 32 + 8 * (lane >> 4));
+        const long long row = t * 32 + (lane & 31);
+        const int first = 32 * (lane >> 5) + 16 * half;  // input within the group
+        const uint2 w = *reinterpret_cast<const uint2 *>(src + row * (k / 2) + g * 32 + first / 2);
         uint32_t out[3] = {0u, 0u, 0u};
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
@@ -117,6 +121,21 @@ __global__ void relayout_w4a4_fp6_codes(const uint8_t *__restrict__ src, uint8_t
         *reinterpret_cast<uint32_t *>(d) = out[0];
         *reinterpret_cast<uint32_t *>(d + 4) = out[1];
         *reinterpret_cast<uint32_t *>(d + 8) = out[2];
+    }
+}
+
+// W4A4 fp6-path weight scales: [N/32][G][32] (tile, group, row).
+__global__ void relayout_fp6_weight_scales(const uint16_t *__restrict__ scales, uint16_t *__restrict__ tiled, int n,
+                                           int k) {
+    const int groups = k / GROUP;
+    const long long total = static_cast<long long>(n) * groups;
+    for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += static_cast<long long>(gridDim.x) * blockDim.x) {
+        const int r = static_cast<int>(i % 32);
+        const long long tg = i / 32;
+        const int g = static_cast<int>(tg % groups);
+        const long long t = tg / groups;
+        tiled[i] = scales[(t * 32 + r) * groups + g];
     }
 }
 
@@ -199,14 +218,13 @@ QI_API int qi_hip_relayout_w4a16_inverse(const void *tiled_codes, const void *ti
 
 QI_API int qi_hip_relayout_w4a4_fp6(const void *codes, const void *scales, void *codes6, void *tiled_scales, int n,
                                     int k, void *stream) {
-    if (n <= 0 || k <= 0 || n % 16 || k % 256 || !codes || !scales || !codes6 || !tiled_scales) return kInvalid;
+    if (n <= 0 || k <= 0 || n % 32 || k % 256 || !codes || !scales || !codes6 || !tiled_scales) return kInvalid;
     if (!aligned(codes, 8) || !aligned(codes6, 4) || !aligned(scales, 2) || !aligned(tiled_scales, 2)) return kInvalid;
     hipStream_t s = stream_of(stream);
-    const long long lanes = static_cast<long long>(n / 16) * (k / GROUP) * WAVE;
-    relayout_w4a4_fp6_codes<<<grid_for(lanes, 256), 256, 0, s>>>(static_cast<const uint8_t *>(codes),
+    const long long slots = static_cast<long long>(n / 32) * (k / GROUP) * 2 * WAVE;
+    relayout_w4a4_fp6_codes<<<grid_for(slots, 256), 256, 0, s>>>(static_cast<const uint8_t *>(codes),
                                                                   static_cast<uint8_t *>(codes6), n, k);
-    relayout_scales<<<grid_for(static_cast<long long>(n) * (k / GROUP), 256), 256, 0, s>>>(
-        static_cast<const uint16_t *>(scales), nullptr, static_cast<uint16_t *>(tiled_scales), n, k, 0, nullptr,
-        nullptr);
+    relayout_fp6_weight_scales<<<grid_for(static_cast<long long>(n) * (k / GROUP), 256), 256, 0, s>>>(
+        static_cast<const uint16_t *>(scales), static_cast<uint16_t *>(tiled_scales), n, k);
     return launch_status();
 }

@@ -4,159 +4,226 @@
 //   y[m, n] = sum over ascending groups g of fmaf(P_g[m, n], sa[m, g] * sw[n, g], y)
 // with P_g the exact integer dot product of the int4 codes of group g.
 //
-// Why fp6.  Every int4 code -7..7 is exact in E2M3, products of two codes are
-// exact, and a K-slice of 64 codes sums to at most 64 * 49 = 3136, so the
-// f8f6f4 MFMA returns P_g exactly, already as fp32 (checked against the int8
-// MFMA on the same codes).  One v_mfma_scale_f32_16x16x128_f8f6f4 covers one
-// 64-group in half of its 128 K-slots (the weight operand's upper slots are
-// zero) at the same cost as one v_mfma_i32_16x16x64_i8, but it saves the
-// int -> float conversion in the per-group fp32 step, which is the bottleneck
-// of W4A4 on this chip: a wave64 fp32 VALU instruction costs 4 cycles and
-// overlaps little with the matrix core.  The scale products sa * sw (exact in
-// fp32: two 11-bit significands) come from a v_mfma_f32_4x4x1_16b_f32 outer
-// product, so the VALU does only the fma per output.  Results are
-// bit-identical to the reference formula, like the int8 kernel's.
+// Why fp6 and 32x32x64.  Every int4 code -7..7 is exact in E2M3, products of
+// two codes are exact, and a group of 64 products sums to at most
+// 64 * 49 = 3136 < 2^24, so v_mfma_scale_f32_32x32x64_f8f6f4 (block scales
+// 2^0) returns P_g exactly, already as fp32.  Its K = 64 is exactly one g64
+// group with no padding, and at the fp6 rate it does the work of two int8
+// 16x16x64 MFMAs per 16 cycles, so the matrix core is no longer the limit:
+// the exact per-group fp32 step (one fma per output per group, with
+// sa * sw formed exactly by v_mfma_f32_32x32x1_2b_f32 outer products) is.
+// Results are bit-identical to the reference formula.
 //
-// Layouts (produced by qi_hip_w4a4_quantize_activations_fp6 and
-// qi_hip_relayout_w4a4_fp6): per 16-row tile t and group g, 768 bytes =
-// 64 lanes x 12 bytes of MFMA operand, lane q*16 + r holding the 16 E2M3 codes
-// of inputs 16q..16q+15 of row 16t + r; scales per (t, g) as 16 fp16.
+// Layouts (written by qi_hip_w4a4_quantize_activations_fp6 and
+// qi_hip_relayout_w4a4_fp6): per 32-row tile T and group g, 1536 bytes = two
+// halves of 64 lanes x 12 bytes; lane l of half h holds the E2M3 codes of
+// inputs 32 * (l / 32) + 16h .. + 15 of row 32T + l % 32, which is the lane's
+// MFMA operand (6 dwords) split in two.  Scales [rows/32][G][32] fp16 for
+// both operands.
 //
-// Roles.  The MFMA A operand is the weight tile (16 outputs n) and B the
-// activation tile (16 rows m), so a lane accumulates four consecutive outputs
-// n of one row m and stores them with one wide write.
+// Roles.  The MFMA A operand is the weight tile (32 outputs n), B the
+// activation tile (32 rows m).  Lane l's accumulator register 4a + r then
+// holds y[m = l % 32][n = 8a + 4 * (l / 32) + r]: four consecutive outputs,
+// stored with one wide write.
 //
 // Pipeline.  A ring of NSTAGE LDS slots holds the operand blocks of upcoming
-// groups, filled with 12-byte-per-lane buffer_load ... lds (one instruction =
-// one 768-byte tile block, which lands in LDS at a 16-byte lane pitch),
-// NSTAGE-1 groups ahead; the scales ride in a
-// register ring.  One barrier per group.
+// groups, filled NSTAGE-1 groups ahead by 12-byte-per-lane
+// buffer_load ... lds (one instruction per 768-byte half block; the data
+// lands at a 16-byte lane pitch); the scales ride in a register ring.  One
+// barrier per group.
+
+#include <utility>
 
 #include "qi_common.h"
 
 namespace qi {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v3i __attribute__((ext_vector_type(3)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ void buffer_load_lds12(__amdgpu_buffer_rsrc_t rsrc, void *lds, uint32_t voffset,
-                                                  uint32_t soffset) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)lds, 12, voffset,
-                                             soffset, 0, 0);
+typedef int v4i_rsrc __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource (base, size in bytes; loads past the end return zero)
+// as four scalar dwords for the inline loads below.
+__device__ __forceinline__ v4i_rsrc raw_rsrc(const void *p, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    return v4i_rsrc{static_cast<int>(a), static_cast<int>((a >> 32) & 0xFFFF), static_cast<int>(bytes), 0x00020000};
 }
 
-template <int TM, int TN, int WM, int WN>
+// Direct-to-LDS buffer loads, written as inline asm so the compiler does not
+// track them: it would otherwise make every LDS read and every barrier wait
+// for all of them, including the loads of later groups into other slots.
+// Their completion is counted explicitly with s_waitcnt vmcnt.  Lane i's
+// data lands at lds_addr + 16 i (12-byte form) or + 4 i (4-byte form).
+// Nothing else in these kernels uses M0.
+__device__ __forceinline__ void dma_dwordx3(v4i_rsrc rsrc, uint32_t lds_addr, uint32_t voffset, uint32_t soffset) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx3 %1, %2, %3 offen lds" ::"s"(lds_addr),
+                 "v"(voffset), "s"(rsrc), "s"(soffset)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ void dma_dword(v4i_rsrc rsrc, uint32_t lds_addr, uint32_t voffset, uint32_t soffset) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds" ::"s"(lds_addr),
+                 "v"(voffset), "s"(rsrc), "s"(soffset)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_address(const void *p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint8_t *)p));
+}
+
+// f(std::integral_constant<int, I>) for I = 0 .. N-1, in order.
+template <int N, typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
+}
+
+// The MFMA reads six dwords of an fp6 operand; the last two are don't-care.
+__device__ __forceinline__ v8i fp6_operand(v3i lo, v3i hi) {
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, -1, -1);
+}
+
+template <int TM, int TN, int WM, int WN, int NSTAGE>
 __global__ __launch_bounds__(WM *WN *WAVE, 2) void w4a4_fp6_kernel(
     const uint8_t *__restrict__ a6, const uint16_t *__restrict__ sa_t, const uint8_t *__restrict__ w6,
     const uint16_t *__restrict__ sw_t, const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi,
     int m, int n, int k) {
-    constexpr int NSTAGE = 4;
     constexpr int NW = WM * WN;
-    constexpr int MT = WM * TM, NTL = WN * TN;  // 16-row tiles of the block
-    constexpr int BM = MT * 16, BN = NTL * 16;
-    static_assert((MT + NTL) % NW == 0, "loader mapping");
-    constexpr int L_PER_W = (MT + NTL) / NW;
-    constexpr int LOADS_PER_GROUP = L_PER_W + TM + TN;  // per wave
-    // A 12-byte direct-to-LDS load writes lane i's bytes at offset 16 * i.
-    __shared__ __attribute__((aligned(16))) uint8_t lds_x[NSTAGE][MT][1024];
-    __shared__ __attribute__((aligned(16))) uint8_t lds_w[NSTAGE][NTL][1024];
+    constexpr int MT = WM * TM, NTL = WN * TN;  // 32-row tiles of the block
+    constexpr int BM = MT * 32, BN = NTL * 32;
+    constexpr int HALVES = 2 * (MT + NTL);      // 768-byte loads per group
+    static_assert(HALVES % NW == 0, "loader mapping");
+    constexpr int L_PER_W = HALVES / NW;
+    static_assert((2 * MT) % L_PER_W == 0, "a wave's loads come from one operand");
+    static_assert(TM <= 4 && TN == 2, "one scale load per operand per wave; scale products pair the n-tiles");
+    constexpr int LOADS_PER_GROUP = L_PER_W + 2;  // per wave: operands + sa + sw
+    constexpr int TILE = 2048, SLOT = (MT + NTL) * TILE;
+    constexpr int SC_WAVE = 512, SC_SLOT = NW * SC_WAVE;  // scale bytes per wave / per slot
+    static_assert(NSTAGE * SLOT <= 65536 && NSTAGE * SC_SLOT <= 65536, "LDS offsets");
+    __shared__ __attribute__((aligned(16))) uint8_t lds[NSTAGE * SLOT];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_sc[NSTAGE * SC_SLOT];
 
     const int groups = k >> 6;
-    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WN, wn = wave % WN;
-    const int r16 = lane & 15;
+    const int r32 = lane & 31;
     const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
     int tm, tn;
     tile_of_block(blockIdx.x, tiles_m, tiles_n, 8, tm, tn);
-    const int mt0 = tm * MT, nt0 = tn * NTL;  // first 16-row tiles
-    const int m_tiles = (m + 15) / 16, n_tiles = n / 16;
+    const int mt0 = tm * MT, nt0 = tn * NTL;  // first 32-row tiles
+    const int m_tiles = (m + 31) / 32, n_tiles = n / 32;
 
-    const uint32_t a_bytes = static_cast<uint32_t>(m_tiles) * groups * 768u;
-    const uint32_t w_bytes = static_cast<uint32_t>(n_tiles) * groups * 768u;
-    const uint32_t sa_bytes = static_cast<uint32_t>(m_tiles) * groups * 32u;
-    const uint32_t sw_bytes = static_cast<uint32_t>(n_tiles) * groups * 32u;
-    const auto ra = buffer_rsrc(a6, a_bytes);
-    const auto rw = buffer_rsrc(w6, w_bytes);
-    const auto rsa = buffer_rsrc(sa_t, sa_bytes);
-    const auto rsw = buffer_rsrc(sw_t, sw_bytes);
+    const uint32_t a_bytes = static_cast<uint32_t>(m_tiles) * groups * 1536u;
+    const uint32_t w_bytes = static_cast<uint32_t>(n_tiles) * groups * 1536u;
+    const v4i_rsrc ra = raw_rsrc(a6, a_bytes);
+    const v4i_rsrc rw = raw_rsrc(w6, w_bytes);
+    const v4i_rsrc rsa = raw_rsrc(sa_t, static_cast<uint32_t>(m_tiles) * groups * 64u);
+    const v4i_rsrc rsw = raw_rsrc(sw_t, static_cast<uint32_t>(n_tiles) * groups * 64u);
 
-    // Operand block loads: instruction I < MT is m-tile I, else n-tile I - MT.
+    // This wave's operand loads: half blocks H0 .. H0 + L_PER_W - 1 of the
+    // block's (MT + NTL) tiles, activation tiles first.  Missing tiles read
+    // past the buffer end, which returns zeros.
+    const int H0 = wave * L_PER_W;
+    const bool from_a = H0 < 2 * MT;
+    const v4i_rsrc rsrc = from_a ? ra : rw;
     uint32_t vo[L_PER_W];
 #pragma unroll
     for (int u = 0; u < L_PER_W; ++u) {
-        const int I = wave * L_PER_W + u;
-        if (I < MT) {
-            const int t = mt0 + I;
-            vo[u] = t < m_tiles ? static_cast<uint32_t>(t) * groups * 768u + lane * 12u : a_bytes;
-        } else {
-            const int t = nt0 + I - MT;
-            vo[u] = t < n_tiles ? static_cast<uint32_t>(t) * groups * 768u + lane * 12u : w_bytes;
-        }
+        const int H = H0 + u, X = H >> 1, half = H & 1;
+        const int t = from_a ? mt0 + X : nt0 + X - MT;
+        const bool ok = from_a ? t < m_tiles : t < n_tiles;
+        vo[u] = ok ? static_cast<uint32_t>(t) * groups * 1536u + half * 768u + lane * 12u
+                   : (from_a ? a_bytes : w_bytes);
     }
-    // Scale operands of the 4x4x1 outer product: the weight lane value is
-    // sw[4 * (lane / 16) + lane % 4], the activation lane value sa[lane % 16].
-    uint32_t sa_vo[TM], sw_vo[TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-        const int t = mt0 + wm * TM + i;
-        sa_vo[i] = t < m_tiles ? (static_cast<uint32_t>(t) * groups * 16u + r16) * 2u : sa_bytes;
-    }
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int t = nt0 + wn * TN + j;
-        sw_vo[j] = t < n_tiles ? (static_cast<uint32_t>(t) * groups * 16u + 4 * (lane >> 4) + (lane & 3)) * 2u
-                               : sw_bytes;
+    // Scales, also loaded straight into LDS (so that every vector-memory load
+    // of the loop is a direct-to-LDS load whose completion this code counts
+    // itself): per wave and group, one 4-byte-per-lane load gathers the 64
+    // bytes of each of its TM activation tiles (lanes 16i .. 16i+15) and one
+    // those of its TN weight tiles.  Lanes past TM / TN read zeros.
+    uint32_t sa_vo, sw_vo;
+    {
+        const int i = lane >> 4, t = mt0 + wm * TM + i;
+        sa_vo = i < TM && t < m_tiles ? static_cast<uint32_t>(t) * groups * 64u + (lane & 15) * 4u : 0x7FFFFFF0u;
+        const int tw = nt0 + wn * TN + i;
+        sw_vo = i < TN && tw < n_tiles ? static_cast<uint32_t>(tw) * groups * 64u + (lane & 15) * 4u : 0x7FFFFFF0u;
     }
 
-    uint32_t sa_ring[NSTAGE][TM], sw_ring[NSTAGE][TN];
+    const uint32_t lds0 = lds_address(lds), sc0 = lds_address(lds_sc);
     auto issue = [&](int g, int slot) {
 #pragma unroll
         for (int u = 0; u < L_PER_W; ++u) {
-            const int I = wave * L_PER_W + u;
-            if (I < MT)
-                buffer_load_lds12(ra, &lds_x[slot][I][0], vo[u], g * 768);
-            else
-                buffer_load_lds12(rw, &lds_w[slot][I - MT][0], vo[u], g * 768);
+            const int H = H0 + u;
+            dma_dwordx3(rsrc, lds0 + slot * SLOT + (H >> 1) * TILE + (H & 1) * 1024, vo[u], g * 1536);
         }
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-            sa_ring[slot][i] = __builtin_amdgcn_raw_buffer_load_b16(rsa, sa_vo[i], g * 32, 0);
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-            sw_ring[slot][j] = __builtin_amdgcn_raw_buffer_load_b16(rsw, sw_vo[j], g * 32, 0);
+        dma_dword(rsa, sc0 + slot * SC_SLOT + wave * SC_WAVE, sa_vo, g * 64);
+        dma_dword(rsw, sc0 + slot * SC_SLOT + wave * SC_WAVE + 256, sw_vo, g * 64);
     };
 
-    v4f acc[TN][TM];
+    v16f acc[TN][TM];
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int i = 0; i < TM; ++i) acc[j][i] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
 
-    auto compute = [&](int slot) {
+    // This lane's fragments: weight tile j half h at
+    // lds[slot][MT + wn * TN + j][h][16 lane], activation tile i likewise.
+    // Scales inside the wave's scale block: sa of row l % 32 of tile i at
+    // 64i + 2 (l % 32); the weight scale at 256 + 64 (l / 32) + 2 (l % 32),
+    // i.e. output l % 32 of n-tile l / 32.
+    const uint8_t *w_frag = lds + (MT + wn * TN) * TILE + lane * 16;
+    const uint8_t *x_frag = lds + wm * TM * TILE + lane * 16;
+    const uint8_t *sa_lds = lds_sc + wave * SC_WAVE + r32 * 2;
+    const uint8_t *sw_lds = lds_sc + wave * SC_WAVE + 256 + lane * 2;
+
+    auto compute = [&](auto slot_c) {
+        constexpr int slot = decltype(slot_c)::value;
         v8i wf[TN], xf[TM];
-        float swl[TN], sal[TM];
+        float sal[TM];
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const uint32_t *p = reinterpret_cast<const uint32_t *>(&lds_w[slot][wn * TN + j][lane * 16]);
-            wf[j] = v8i{static_cast<int>(p[0]), static_cast<int>(p[1]), static_cast<int>(p[2]), 0, 0, 0, 0, 0};
-            swl[j] = h2f(static_cast<uint16_t>(sw_ring[slot][j]));
+            const v3i lo = *reinterpret_cast<const v3i *>(w_frag + slot * SLOT + j * TILE);
+            const v3i hi = *reinterpret_cast<const v3i *>(w_frag + slot * SLOT + j * TILE + 1024);
+            wf[j] = fp6_operand(lo, hi);
         }
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
-            const uint32_t *p = reinterpret_cast<const uint32_t *>(&lds_x[slot][wm * TM + i][lane * 16]);
-            xf[i] = v8i{static_cast<int>(p[0]), static_cast<int>(p[1]), static_cast<int>(p[2]), 0, 0, 0, 0, 0};
-            sal[i] = h2f(static_cast<uint16_t>(sa_ring[slot][i]));
+            const v3i lo = *reinterpret_cast<const v3i *>(x_frag + slot * SLOT + i * TILE);
+            const v3i hi = *reinterpret_cast<const v3i *>(x_frag + slot * SLOT + i * TILE + 1024);
+            xf[i] = fp6_operand(lo, hi);
+            sal[i] = h2f(*reinterpret_cast<const uint16_t *>(sa_lds + slot * SC_SLOT + 64 * i));
         }
+        const float swl = h2f(*reinterpret_cast<const uint16_t *>(sw_lds + slot * SC_SLOT));
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+        for (int i = 0; i < TM; ++i) {
+            // sa * sw for both n-tiles: block b of the 32x32x1 outer product
+            // has rows = outputs of n-tile b (lanes 32b .. 32b+31 supply
+            // them) and columns = rows m of tile i; its 16 result registers
+            // 16b .. 16b+15 line up with the accumulator registers.
+            v32f z32;
 #pragma unroll
-            for (int i = 0; i < TM; ++i) {
+            for (int r = 0; r < 32; ++r) z32[r] = 0.f;
+            const v32f sp = __builtin_amdgcn_mfma_f32_32x32x1f32(swl, sal[i], z32, 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                v16f z;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) z[r] = 0.f;
                 // fmt 2 = FP6 E2M3 for both operands; block scales 2^0.
-                const v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[j], xf[i], v4f{0.f, 0.f, 0.f, 0.f},
-                                                                             2, 2, 0, 127, 0, 127);
-                const v4f s = __builtin_amdgcn_mfma_f32_4x4x1f32(swl[j], sal[i], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                const v16f p = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[j], xf[i], z, 2, 2, 0, 127, 0, 127);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) acc[j][i][r] = __builtin_fmaf(p[r], s[r], acc[j][i][r]);
+                for (int r = 0; r < 16; ++r) acc[j][i][r] = __builtin_fmaf(p[r], sp[16 * j + r], acc[j][i][r]);
             }
+        }
     };
 
     // Prologue; loads past the last group read harmless bytes into slots
@@ -164,51 +231,60 @@ __global__ __launch_bounds__(WM *WN *WAVE, 2) void w4a4_fp6_kernel(
 #pragma unroll
     for (int p = 0; p < NSTAGE - 1; ++p) issue(p, p);
     for (int g0 = 0; g0 < groups; g0 += NSTAGE) {
-#pragma unroll
-        for (int u = 0; u < NSTAGE; ++u) {
+        static_for<NSTAGE>([&](auto uc) {
+            constexpr int u = decltype(uc)::value;
             const int g = g0 + u;
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTAGE - 2) * LOADS_PER_GROUP) : "memory");
-            __syncthreads();
+            // This wave's loads of group g are done; after the barrier so are
+            // every wave's, and every wave has finished reading the slot the
+            // next issue overwrites (compute ends with lgkmcnt(0)).  A bare
+            // s_barrier: __syncthreads' release fence would also wait for
+            // the loads of the groups still in flight.
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((NSTAGE - 2) * LOADS_PER_GROUP) : "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
             issue(g + NSTAGE - 1, (u + NSTAGE - 1) % NSTAGE);
-            if (g < groups) compute(u);
-        }
+            if (g < groups) compute(uc);
+        });
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-    // acc[j][i][r] = y[row, col]: row = m-tile i, lane % 16; col = n-tile j,
-    // 4 * (lane / 16) + r.
-    const int q = lane >> 4;
+    // acc[j][i][4a + r] = y[row, col]: row = m-tile i, lane % 32; col = n-tile
+    // j, 8a + 4 * (lane / 32) + r.
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int col = (nt0 + wn * TN + j) * 16 + 4 * q;
-        if (col >= n) continue;
+    for (int i = 0; i < TM; ++i) {
+        const int row = (mt0 + wm * TM + i) * 32 + r32;
+        if (row >= m) continue;
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            const int row = (mt0 + wm * TM + i) * 16 + r16;
-            if (row >= m) continue;
-            float v[4];
+        for (int j = 0; j < TN; ++j) {
+            const int tile_col = (nt0 + wn * TN + j) * 32;
+            if (tile_col >= n) continue;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) v[r] = epilogue(acc[j][i][r], bias, col + r, epi);
-            const size_t idx = static_cast<size_t>(row) * n + col;
-            if (out_type == QI_HIP_OUT_F16) {
-                uint2 h;
-                h.x = static_cast<uint32_t>(f2h(v[0])) | (static_cast<uint32_t>(f2h(v[1])) << 16);
-                h.y = static_cast<uint32_t>(f2h(v[2])) | (static_cast<uint32_t>(f2h(v[3])) << 16);
-                *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(y) + idx) = h;
-            } else {
-                *reinterpret_cast<float4 *>(reinterpret_cast<float *>(y) + idx) = float4{v[0], v[1], v[2], v[3]};
+            for (int a = 0; a < 4; ++a) {
+                const int col = tile_col + 8 * a + 4 * (lane >> 5);
+                float v[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[r] = epilogue(acc[j][i][4 * a + r], bias, col + r, epi);
+                const size_t idx = static_cast<size_t>(row) * n + col;
+                if (out_type == QI_HIP_OUT_F16) {
+                    uint2 h;
+                    h.x = static_cast<uint32_t>(f2h(v[0])) | (static_cast<uint32_t>(f2h(v[1])) << 16);
+                    h.y = static_cast<uint32_t>(f2h(v[2])) | (static_cast<uint32_t>(f2h(v[3])) << 16);
+                    *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(y) + idx) = h;
+                } else {
+                    *reinterpret_cast<float4 *>(reinterpret_cast<float *>(y) + idx) = float4{v[0], v[1], v[2], v[3]};
+                }
             }
         }
     }
 }
 
-template <int TM, int TN, int WM, int WN>
+template <int TM, int TN, int WM, int WN, int NSTAGE>
 static int launch_fp6(const void *a6, const void *sa, const void *w6, const void *sw, const float *bias, void *y,
                       int out_type, int epi, int m, int n, int k, hipStream_t stream) {
-    constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
+    constexpr int BM = WM * TM * 32, BN = WN * TN * 32;
     const long long blocks = static_cast<long long>((m + BM - 1) / BM) * ((n + BN - 1) / BN);
     if (blocks > 0x7FFFFFFFLL) return kInvalid;
-    w4a4_fp6_kernel<TM, TN, WM, WN><<<dim3(static_cast<unsigned>(blocks)), dim3(WM * WN * WAVE), 0, stream>>>(
+    w4a4_fp6_kernel<TM, TN, WM, WN, NSTAGE><<<dim3(static_cast<unsigned>(blocks)), dim3(WM * WN * WAVE), 0, stream>>>(
         static_cast<const uint8_t *>(a6), static_cast<const uint16_t *>(sa), static_cast<const uint8_t *>(w6),
         static_cast<const uint16_t *>(sw), bias, y, out_type, epi, m, n, k);
     return launch_status();
@@ -221,20 +297,19 @@ using namespace qi;
 QI_API int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *a_scales_tiled, const void *w_codes6,
                                 const void *w_scales_tiled, const float *bias, void *y, int out_type, int epilogue,
                                 int m, int n, int k, void *stream) {
-    if (m <= 0 || n <= 0 || k <= 0 || n % 16 || k % 256) return kInvalid;
+    if (m <= 0 || n <= 0 || k <= 0 || n % 32 || k % 256) return kInvalid;
     if (!a_codes6 || !a_scales_tiled || !w_codes6 || !w_scales_tiled || !y) return kInvalid;
     if (out_type != QI_HIP_OUT_F32 && out_type != QI_HIP_OUT_F16) return kInvalid;
     if (epilogue != QI_HIP_EPILOGUE_NONE && epilogue != QI_HIP_EPILOGUE_GELU_TANH) return kInvalid;
     if (reinterpret_cast<uintptr_t>(a_codes6) % 4 || reinterpret_cast<uintptr_t>(w_codes6) % 4 ||
-        reinterpret_cast<uintptr_t>(a_scales_tiled) % 2 || reinterpret_cast<uintptr_t>(w_scales_tiled) % 2)
+        reinterpret_cast<uintptr_t>(a_scales_tiled) % 2 || reinterpret_cast<uintptr_t>(w_scales_tiled) % 2 ||
+        reinterpret_cast<uintptr_t>(y) % (out_type == QI_HIP_OUT_F16 ? 8 : 16))
         return kInvalid;
     const long long g = k / 64;
-    if (static_cast<long long>((m + 15) / 16) * g * 768 >= (1LL << 32) || static_cast<long long>(n / 16) * g * 768 >= (1LL << 32))
+    if (static_cast<long long>((m + 31) / 32) * g * 1536 >= (1LL << 31) ||
+        static_cast<long long>(n / 32) * g * 1536 >= (1LL << 31))
         return kInvalid;
     hipStream_t s = stream_of(stream);
-    if (m <= 512)
-        return launch_fp6<2, 2, 2, 2>(a_codes6, a_scales_tiled, w_codes6, w_scales_tiled, bias, y, out_type, epilogue, m,
-                                      n, k, s);
-    return launch_fp6<4, 4, 2, 2>(a_codes6, a_scales_tiled, w_codes6, w_scales_tiled, bias, y, out_type, epilogue, m, n,
-                                  k, s);
+    return launch_fp6<2, 2, 2, 2, 4>(a_codes6, a_scales_tiled, w_codes6, w_scales_tiled, bias, y, out_type, epilogue,
+                                     m, n, k, s);
 }

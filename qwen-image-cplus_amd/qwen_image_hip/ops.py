@@ -193,15 +193,15 @@ def w4a16_gemv(x_half, w_tiled_codes, w_tiled_scales, bias=None, out_dtype=torch
 
 
 def fp6_rows(m: int) -> int:
-    """Rows an fp6 activation buffer holds for m rows (whole 16-row tiles)."""
-    return (m + 15) // 16 * 16
+    """Rows an fp6 activation buffer holds for m rows (whole 32-row tiles)."""
+    return (m + 31) // 32 * 32
 
 
 def quantize_activations_fp6(x: torch.Tensor, codes6: torch.Tensor | None = None,
                              scales: torch.Tensor | None = None):
     """Quantise rows of x into the fp6 MFMA-operand layout.
 
-    Returns (codes6 uint8 [ceil(m/16)*16, 3k/4], scales fp16 [ceil(m/16)*16, k/64]) in
+    Returns (codes6 uint8 [ceil(m/32)*32, 3k/4], scales fp16 [ceil(m/32)*32, k/64]) in
     tile order (see qwen_image_hip.h).  Same codes as quantize_activations.
     """
     m, k = x.shape

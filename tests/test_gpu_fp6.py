@@ -26,9 +26,12 @@ def _u16(t):
 
 
 def decode_fp6_tiles(buf: np.ndarray, rows: int, k: int) -> np.ndarray:
-    """fp6 operand tiles [rows/16][G][64 lanes][12 B] -> int codes [rows, k]."""
+    """fp6 operand tiles [rows/32][G][2 halves][64 lanes][12 B] -> int codes [rows, k].
+
+    Lane l of half h holds inputs 32 * (l // 32) + 16h .. + 15 of row l % 32.
+    """
     G = k // 64
-    b = buf.reshape(rows // 16, G, 64, 12).astype(np.uint32)
+    b = buf.reshape(rows // 32, G, 2, 64, 12).astype(np.uint32)
     b = np.concatenate([b, np.zeros(b.shape[:-1] + (1,), np.uint32)], axis=-1)
     vals = np.zeros(b.shape[:-1] + (16,), np.int64)
     lut = np.zeros(64, np.int64)
@@ -40,8 +43,8 @@ def decode_fp6_tiles(buf: np.ndarray, rows: int, k: int) -> np.ndarray:
         byte, shift = bit // 8, bit % 8
         word = b[..., byte] | (b[..., byte + 1] << 8)
         vals[..., j] = lut[(word >> shift) & 63]
-    # [t, g, q, r, j] -> [t, r, g, q, j]
-    v = vals.reshape(rows // 16, G, 4, 16, 16).transpose(0, 3, 1, 2, 4)
+    # [t, g, h, lhi, r, j] -> [t, r, g, lhi, h, j]
+    v = vals.reshape(rows // 32, G, 2, 2, 32, 16).transpose(0, 4, 1, 3, 2, 5)
     return v.reshape(rows, k)
 
 
@@ -51,9 +54,9 @@ def unpack_nibbles(codes: np.ndarray) -> np.ndarray:
 
 
 def tiled_scales(scales: np.ndarray, rows: int) -> np.ndarray:
-    """[rows, G] -> [rows/16][G][16] as stored by the fp6 path."""
+    """[rows, G] -> [rows/32][G][32] as stored by the fp6 path."""
     G = scales.shape[1]
-    return scales.reshape(rows // 16, 16, G).transpose(0, 2, 1).reshape(rows, G)
+    return scales.reshape(rows // 32, 32, G).transpose(0, 2, 1).reshape(rows, G)
 
 
 @pytest.mark.parametrize("m,k,half", [(16, 256, False), (37, 768, True), (128, 3072, False)])
@@ -66,16 +69,13 @@ def test_fp6_quantizer_matches_codes(dev, m, k, half):
     rows = ops.fp6_rows(m)
     codes = decode_fp6_tiles(c6.cpu().numpy(), rows, k)[:m]
     np.testing.assert_array_equal(codes, unpack_nibbles(want_c))
-    pad = np.zeros((rows, k // 64), np.uint16)
-    pad[:m] = want_s
-    got_s = _u16(s6).reshape(rows, k // 64)
-    np.testing.assert_array_equal(tiled_scales(got_s, rows)[:m] if False else got_s.reshape(rows // 16, k // 64, 16)
-                                  .transpose(0, 2, 1).reshape(rows, k // 64)[:m], want_s)
+    got_s = _u16(s6).reshape(rows // 32, k // 64, 32).transpose(0, 2, 1).reshape(rows, k // 64)
+    np.testing.assert_array_equal(got_s[:m], want_s)
 
 
 def test_fp6_weight_relayout(dev):
     import qwen_image_hip.ops as ops
-    n, k = 48, 512
+    n, k = 64, 512
     w = weights_f16(n, k, 41)
     c, s, _ = oracle.quantize_matrix(w, 6, clip=True)
     c6, ts = ops.relayout_w4a4_fp6(_dev(c, dev), _h(s, dev))
@@ -83,7 +83,7 @@ def test_fp6_weight_relayout(dev):
     np.testing.assert_array_equal(_u16(ts).reshape(n, k // 64), tiled_scales(s, n))
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 16, 256), (5, 48, 512), (100, 256, 768), (263, 128, 1024),
+@pytest.mark.parametrize("m,n,k", [(1, 32, 256), (5, 96, 512), (100, 256, 768), (263, 128, 1024),
                                    (640, 1024, 512), (1024, 512, 3072)])
 def test_fp6_gemm_bit_exact(dev, m, n, k):
     print(f"fp6 gemm m={m} n={n} k={k}", flush=True)
@@ -118,6 +118,6 @@ def test_fp6_group_partials_exact(dev):
         s_act[:, g] = 0x3C00
         s_w[:, g] = 0x3C00
         w6, sw = ops.relayout_w4a4_fp6(_dev(wc, dev), _h(s_w, dev))
-        sa_t = _h(tiled_scales(s_act, m), dev)
+        sa_t = _h(tiled_scales(s_act, m), dev)  # m is a multiple of 32
         got = ops.w4a4_gemm_fp6(a6, sa_t, w6, sw, m).cpu().numpy()
         np.testing.assert_array_equal(got, partials[:, :, g].astype(np.float32))
