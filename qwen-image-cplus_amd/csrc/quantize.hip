@@ -7,12 +7,12 @@
 //
 // Design.  The H256 rotation and the 64-groups never cross a 256-element
 // chunk, so a chunk is the unit of work: one wavefront owns one chunk, each
-// lane four consecutive elements (one 16-byte load).  The first butterfly
-// stage (stride 1) runs in registers; strides 4, 16 and 64 go through a
-// 1 KiB wave-private LDS slice.  Lanes 16g..16g+15 then hold group g, reduce
-// its absmax with 16-lane shuffles, and each lane writes two code bytes.  A
-// row of any length is just more chunks, so there is no per-row LDS limit
-// and the grid has m * k / 256 wavefronts to spread over the 256 CUs.
+// lane four consecutive elements (one 8- or 16-byte load).  The first
+// butterfly stage (stride 1) runs in registers; strides 4, 16 and 64 go
+// through a 1 KiB wave-private, bank-swizzled LDS slice without barriers.
+// Lanes 16g..16g+15 then hold group g and reduce its absmax with 16-lane
+// shuffles.  A row of any length is just more chunks, so there is no per-row
+// LDS limit, and the grid has m * k / 256 wavefronts to spread over the CUs.
 
 #include "qi_common.h"
 
@@ -53,85 +53,111 @@ __device__ __forceinline__ void load4<uint16_t>(const uint16_t *src, float v[4])
 //        = 2 halves x 64 lanes x 12 bytes; lane l of half h holds the E2M3
 //        codes (6 bits each, little-endian) of inputs 32 * (l / 32) + 16h ..
 //        + 15 of the group, row 32T + l % 32.  Scales [m/32][G][32] fp16.
-template <typename In, int FMT>
+// LDS word of element i of a chunk: an XOR swizzle that makes every access
+// pattern below (4 consecutive words per lane, and the strided butterfly
+// quadruples of strides 4, 16, 64) conflict-free for 32 lanes at a time.
+__device__ __forceinline__ int swz(int i) { return i ^ ((i >> 2) & 31); }
+
+// E2M3 code of the int4 value q: |q| 0..7 -> 0, 8, 16, 20, 24, 26, 28, 30,
+// i.e. twice the nibble |q| of 0xFEDCA840, plus the sign bit 32.
+__device__ __forceinline__ uint32_t e2m3_of(int q) {
+    const uint32_t a = static_cast<uint32_t>(q < 0 ? -q : q);
+    return (__builtin_amdgcn_ubfe(0xFEDCA840u, 4 * a, 4) << 1) | (q < 0 ? 32u : 0u);
+}
+
+// Grid: x = row, y = group of QUANT_WAVES * CPW chunks of the row.  Wave w
+// of the workgroup owns chunks base + w + QUANT_WAVES * i, i < CPW (chunk c =
+// elements [256c, 256c + 256) of the row); it issues all their loads first
+// and reuses its LDS addressing for each.
+template <typename In, int FMT, int CPW>
 __global__ __launch_bounds__(QUANT_WAVES * WAVE) void quantize_chunks_kernel(
-    const In *__restrict__ x, uint8_t *__restrict__ codes, uint16_t *__restrict__ scales, long long chunks,
-    int chunks_per_row) {
+    const In *__restrict__ x, uint8_t *__restrict__ codes, uint16_t *__restrict__ scales, int k) {
     __shared__ float lds[QUANT_WAVES][256];
     const int lane = threadIdx.x & (WAVE - 1);
     const int wave = threadIdx.x >> 6;
-    const long long chunk = static_cast<long long>(blockIdx.x) * QUANT_WAVES + wave;
-    const bool active = chunk < chunks;
-    float *row = lds[wave];
+    const int chunks_per_row = k >> 8;
+    const int c0 = blockIdx.y * QUANT_WAVES * CPW + wave;
+    if (c0 >= chunks_per_row) return;  // whole wave; no workgroup barrier below
+    const uint32_t row = blockIdx.x;
+    float *buf = lds[wave];
 
-    // Chunk c covers elements [256c, 256c + 256) of the flattened [m, k]
-    // array (k % 256 == 0, so chunks never straddle rows).
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
-    if (active) load4<In>(x + chunk * 256 + lane * 4, v);
-    butterfly4(v[0], v[1], v[2], v[3]);  // stride 1: in registers
-    row[lane * 4 + 0] = v[0];
-    row[lane * 4 + 1] = v[1];
-    row[lane * 4 + 2] = v[2];
-    row[lane * 4 + 3] = v[3];
-    __syncthreads();
+    float in[CPW][4];
 #pragma unroll
-    for (int stride = 4; stride < 256; stride *= 4) {
-        // Lane b owns butterfly b of this stage.
-        const int i0 = (lane / stride) * (stride * 4) + (lane % stride);
-        float a = row[i0], b = row[i0 + stride], c = row[i0 + 2 * stride], d = row[i0 + 3 * stride];
-        butterfly4(a, b, c, d);
-        // A stage's butterflies partition the chunk, so a lane rewrites only
-        // the four elements it just read; the barrier orders the stages.
-        row[i0] = a;
-        row[i0 + stride] = b;
-        row[i0 + 2 * stride] = c;
-        row[i0 + 3 * stride] = d;
-        __syncthreads();
+    for (int i = 0; i < CPW; ++i) {
+        const int c = c0 + QUANT_WAVES * i;
+        if (c < chunks_per_row) load4<In>(x + static_cast<size_t>(row) * k + c * 256 + lane * 4, in[i]);
     }
-    v[0] = row[lane * 4 + 0];
-    v[1] = row[lane * 4 + 1];
-    v[2] = row[lane * 4 + 2];
-    v[3] = row[lane * 4 + 3];
+#pragma unroll
+    for (int i = 0; i < CPW; ++i) {
+        const int c = c0 + QUANT_WAVES * i;
+        if (c >= chunks_per_row) break;
+        float v[4] = {in[i][0], in[i][1], in[i][2], in[i][3]};
+        butterfly4(v[0], v[1], v[2], v[3]);  // stride 1: in registers
+#pragma unroll
+        for (int j = 0; j < 4; ++j) buf[swz(lane * 4 + j)] = v[j];
+        // The chunk belongs to this wave alone, and a wave's LDS accesses
+        // execute in order, so the stages need no barrier -- only a compiler
+        // fence.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int stride = 4; stride < 256; stride *= 4) {
+            // Lane b owns butterfly b of this stage.
+            const int i0 = (lane / stride) * (stride * 4) + (lane % stride);
+            float a = buf[swz(i0)], b = buf[swz(i0 + stride)], cc = buf[swz(i0 + 2 * stride)],
+                  d = buf[swz(i0 + 3 * stride)];
+            butterfly4(a, b, cc, d);
+            // A stage's butterflies partition the chunk, so a lane rewrites
+            // only the four elements it just read.
+            buf[swz(i0)] = a;
+            buf[swz(i0 + stride)] = b;
+            buf[swz(i0 + 2 * stride)] = cc;
+            buf[swz(i0 + 3 * stride)] = d;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = buf[swz(lane * 4 + j)];
+        // The next chunk's first writes must follow these reads.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
 
-    // Group g of the chunk = lanes 16g .. 16g+15.  absmax is order-free.
-    float peak = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        // Group g of the chunk = lanes 16g .. 16g+15.  absmax is order-free.
+        float peak = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
 #pragma unroll
-    for (int s = 8; s > 0; s >>= 1) peak = fmaxf(peak, __shfl_xor(peak, s, 64));
-    // gemm.cu:45-48: IEEE division by 7, fp16 RNE scale, IEEE v / scale,
-    // rint (nearest even), clamp to [-7, 7].
-    const uint16_t scale_bits = f2h(fmaxf(peak / 7.0f, 5.9604645e-08f));
-    const float scale = h2f(scale_bits);
-    int c[4];
+        for (int s = 8; s > 0; s >>= 1) peak = fmaxf(peak, __shfl_xor(peak, s, 64));
+        // gemm.cu:45-48: IEEE division by 7, fp16 RNE scale, IEEE v / scale,
+        // rint (nearest even), clamp to [-7, 7].
+        const uint16_t scale_bits = f2h(fmaxf(peak / 7.0f, 5.9604645e-08f));
+        const float scale = h2f(scale_bits);
+        int q[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) c[j] = static_cast<int>(fminf(fmaxf(rintf(v[j] / scale), -7.0f), 7.0f));
-    if (active) {
+        for (int j = 0; j < 4; ++j) q[j] = static_cast<int>(fminf(fmaxf(rintf(v[j] / scale), -7.0f), 7.0f));
+        const int g = c * 4 + (lane >> 4);  // group within the row
         if (FMT == 0) {
-            const uint16_t packed = static_cast<uint16_t>((c[0] & 0xF) | ((c[1] & 0xF) << 4) | ((c[2] & 0xF) << 8) |
-                                                          ((c[3] & 0xF) << 12));
-            reinterpret_cast<uint16_t *>(codes)[chunk * 64 + lane] = packed;
-            if ((lane & 15) == 0) scales[chunk * 4 + (lane >> 4)] = scale_bits;
+            const uint16_t packed = static_cast<uint16_t>((q[0] & 0xF) | ((q[1] & 0xF) << 4) | ((q[2] & 0xF) << 8) |
+                                                          ((q[3] & 0xF) << 12));
+            reinterpret_cast<uint16_t *>(codes)[static_cast<size_t>(row) * (k >> 2) + c * 64 + lane] = packed;
+            if ((lane & 15) == 0) scales[static_cast<size_t>(row) * (k >> 6) + g] = scale_bits;
         } else {
-            // This lane's four inputs are 4p..4p+3 of slice q of group g
-            // (inputs 16q..16q+15).  Slice q goes to half q & 1 of the
-            // (32-row tile, group) block, lane slot 32 * (q >> 1) + row % 32,
-            // whose 12 bytes are the 24-bit runs of lanes p = 0..3: lane p
-            // < 3 assembles and stores dword p.
-            const long long row = chunk / chunks_per_row;
-            const int groups = chunks_per_row * 4;
-            const int g = static_cast<int>(chunk % chunks_per_row) * 4 + (lane >> 4);
-            const int q = (lane & 15) >> 2, p = lane & 3;
-            const uint32_t bits = int4_to_e2m3(c[0]) | (int4_to_e2m3(c[1]) << 6) | (int4_to_e2m3(c[2]) << 12) |
-                                  (int4_to_e2m3(c[3]) << 18);
+            // This lane's four inputs are 4p..4p+3 of slice sl of group g
+            // (inputs 16 sl .. 16 sl + 15).  Slice sl goes to half sl & 1 of
+            // the (32-row tile, group) block, lane slot 32 (sl >> 1) + row %
+            // 32, whose 12 bytes are the 24-bit runs of lanes p = 0..3: lane
+            // p < 3 assembles and stores dword p.
+            const int sl = (lane & 15) >> 2, p = lane & 3;
+            const uint32_t bits =
+                e2m3_of(q[0]) | (e2m3_of(q[1]) << 6) | (e2m3_of(q[2]) << 12) | (e2m3_of(q[3]) << 18);
             const uint32_t next = static_cast<uint32_t>(__shfl_down(static_cast<int>(bits), 1, 64));
-            const long long block = (row >> 5) * groups + g;
-            const int r32 = static_cast<int>(row & 31);
+            const uint32_t block = (row >> 5) * (k >> 6) + g;
+            const uint32_t r32 = row & 31;
             if (p < 3) {
                 const uint32_t word = (bits >> (8 * p)) | (next << (24 - 8 * p));
-                uint32_t *dst = reinterpret_cast<uint32_t *>(codes + block * 1536 + (q & 1) * 768 +
-                                                             ((q >> 1) * 32 + r32) * 12);
+                uint32_t *dst = reinterpret_cast<uint32_t *>(codes + static_cast<size_t>(block) * 1536 +
+                                                             (sl & 1) * 768 + ((sl >> 1) * 32 + r32) * 12);
                 dst[p] = word;
             }
-            if ((lane & 15) == 0) scales[block * 32 + r32] = scale_bits;
+            if ((lane & 15) == 0) scales[static_cast<size_t>(block) * 32 + r32] = scale_bits;
         }
     }
 }
@@ -163,11 +189,22 @@ static int launch_quantize(const In *x, void *codes, void *scales, int m, int k,
         reinterpret_cast<uintptr_t>(codes) % (FMT == 0 ? 2 : 4) != 0 ||
         reinterpret_cast<uintptr_t>(scales) % 2 != 0)
         return kInvalid;
-    const long long chunks = static_cast<long long>(m) * (k / 256);
-    const long long blocks = (chunks + QUANT_WAVES - 1) / QUANT_WAVES;
-    if (blocks > 0x7FFFFFFFLL) return kInvalid;
-    quantize_chunks_kernel<In, FMT><<<dim3(static_cast<unsigned>(blocks)), dim3(QUANT_WAVES * WAVE), 0, stream>>>(
-        x, static_cast<uint8_t *>(codes), static_cast<uint16_t *>(scales), chunks, k / 256);
+    // Several chunks per wave when there are rows enough to fill the chip.
+    const int chunks = k / 256;
+    if (m >= 1024) {
+        constexpr int CPW = 4;
+        const int chunk_groups = (chunks + QUANT_WAVES * CPW - 1) / (QUANT_WAVES * CPW);
+        if (chunk_groups > 65535) return kInvalid;
+        quantize_chunks_kernel<In, FMT, CPW><<<dim3(static_cast<unsigned>(m), chunk_groups), dim3(QUANT_WAVES * WAVE),
+                                               0, stream>>>(x, static_cast<uint8_t *>(codes),
+                                                            static_cast<uint16_t *>(scales), k);
+    } else {
+        const int chunk_groups = (chunks + QUANT_WAVES - 1) / QUANT_WAVES;
+        if (chunk_groups > 65535) return kInvalid;
+        quantize_chunks_kernel<In, FMT, 1><<<dim3(static_cast<unsigned>(m), chunk_groups), dim3(QUANT_WAVES * WAVE), 0,
+                                             stream>>>(x, static_cast<uint8_t *>(codes),
+                                                       static_cast<uint16_t *>(scales), k);
+    }
     return launch_status();
 }
 

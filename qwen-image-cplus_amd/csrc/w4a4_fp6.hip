@@ -203,27 +203,37 @@ __global__ __launch_bounds__(WM *WN *WAVE, 2) void w4a4_fp6_kernel(
             sal[i] = h2f(*reinterpret_cast<const uint16_t *>(sa_lds + slot * SC_SLOT + 64 * i));
         }
         const float swl = h2f(*reinterpret_cast<const uint16_t *>(sw_lds + slot * SC_SLOT));
+        // All matrix-core work of the group first (scale outer products,
+        // then the four partial tiles), so the matrix core runs while the
+        // fp32 steps of earlier tiles execute.  Block b of the 32x32x1 outer
+        // product has rows = outputs of n-tile b (lanes 32b .. 32b+31 supply
+        // them) and columns = rows m of tile i; its result registers
+        // 16b .. 16b+15 line up with the accumulator registers.
+        v32f sp[TM];
+        v16f p[TN][TM];
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
-            // sa * sw for both n-tiles: block b of the 32x32x1 outer product
-            // has rows = outputs of n-tile b (lanes 32b .. 32b+31 supply
-            // them) and columns = rows m of tile i; its 16 result registers
-            // 16b .. 16b+15 line up with the accumulator registers.
             v32f z32;
 #pragma unroll
             for (int r = 0; r < 32; ++r) z32[r] = 0.f;
-            const v32f sp = __builtin_amdgcn_mfma_f32_32x32x1f32(swl, sal[i], z32, 0, 0, 0);
+            sp[i] = __builtin_amdgcn_mfma_f32_32x32x1f32(swl, sal[i], z32, 0, 0, 0);
+        }
 #pragma unroll
-            for (int j = 0; j < TN; ++j) {
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
                 v16f z;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) z[r] = 0.f;
                 // fmt 2 = FP6 E2M3 for both operands; block scales 2^0.
-                const v16f p = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[j], xf[i], z, 2, 2, 0, 127, 0, 127);
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[j][i][r] = __builtin_fmaf(p[r], sp[16 * j + r], acc[j][i][r]);
+                p[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[j], xf[i], z, 2, 2, 0, 127, 0, 127);
             }
-        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[j][i][r] = __builtin_fmaf(p[j][i][r], sp[i][16 * j + r], acc[j][i][r]);
     };
 
     // Prologue; loads past the last group read harmless bytes into slots
