@@ -4,98 +4,258 @@
 // Arithmetic: W = fp16(fmaf(code, scale, minimum)) exactly as the W4A16 GEMM
 // (qwen_image_cuda/cuda/gemm.cu:222-230), computed two weights per packed
 // fp16 instruction where that is provably the same value; weight x activation
-// pairs accumulate in fp32 with v_dot2 (exact fp16 products).  The reference runs these linears in BF16 through
+// pairs accumulate in fp32 on the matrix core (v_mfma_f32_16x16x32_f16: the
+// tiled code layout is already its A-operand layout).  The reference runs these linears in BF16 through
 // cuBLAS SGEMM (qwen_image_cuda/src/transformer.cplus:716-730); there is no
 // INT4 GEMV there to follow.
 //
 // Design.  One workgroup owns one 16-row weight tile; in the tiled layout the
-// tile's groups are consecutive 512-byte blocks, so the four wavefronts take
-// groups g = w, w+4, ... and the workgroup streams the tile front to back,
-// each lane issuing one 8-byte load per group.  Each lane dequantises its 16
-// weights, multiplies them with the matching activations of every row, and
-// the partial sums are reduced over the four 16-lane k-slices with shuffles
-// and over the wavefronts through LDS.
+// tile's groups are consecutive 512-byte blocks, and each of the four
+// wavefronts streams a contiguous quarter of them, keeping two batches of
+// four groups of loads (one 8-byte code load and one scale pair per lane
+// each) in flight.
+// The activations are first staged in LDS, so the weight stream never waits
+// on them.  Each lane dequantises its 16 weights per group, two MFMAs per
+// group multiply them with up to 16 rows of x, and the wavefronts' partial
+// sums are added through LDS.
 
 #include "qi_common.h"
 
 namespace qi {
 
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
 constexpr int GEMV_WAVES = 4;
-constexpr int GEMV_UNROLL = 4;
+constexpr int GEMV_BATCH = 4;  // groups per batch; two batches are in flight per wave
+constexpr int GEMV_LDS_X = 48 * 1024;  // bytes of activations staged in LDS
 
-template <int MR>
+// XLDS: the workgroup first copies x (m rows x k fp16) into LDS, so the
+// weight stream never waits on activation loads; used when m * k * 2 fits.
+template <bool XLDS>
 __global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
     const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int m, int n, int k) {
-    __shared__ float partial[GEMV_WAVES][MR][16];
+    __shared__ float partial[GEMV_WAVES][16][17];
+    extern __shared__ __attribute__((aligned(16))) uint16_t xs_lds[];  // m * k fp16 when XLDS
     const int groups = k >> 6;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
     const int q = lane >> 4, r16 = lane & 15;
     const int tile = blockIdx.x;
+
+    // Wave w streams groups [g_begin, g_end) of the tile: contiguous
+    // 512-byte code blocks and 64-byte scale blocks.
+    const int per_wave = (groups + GEMV_WAVES - 1) / GEMV_WAVES;
+    const int g_begin = wave * per_wave;
+    const int g_end = min(groups, g_begin + per_wave);
     const uint8_t *cp = codes + static_cast<size_t>(tile) * groups * 512 + lane * 8;
     const uint32_t *sp = reinterpret_cast<const uint32_t *>(scales) + static_cast<size_t>(tile) * groups * 16 + r16;
 
-    float acc[MR];
+    // Batches of GEMV_BATCH groups, double-buffered: the loads of batch b + 1
+    // are issued before batch b is consumed, so every wave overlaps its
+    // dequantisation with its next loads.  The first two batches are
+    // requested before the activations are staged.
+    uint2 c[2][GEMV_BATCH];
+    uint32_t sm[2][GEMV_BATCH];
+    auto load_batch = [&](int b, int g) {
 #pragma unroll
-    for (int r = 0; r < MR; ++r) acc[r] = 0.0f;
-
-    auto consume = [&](int g, uint2 c, uint32_t sm) {
-        const uint32_t sb = sm & 0xFFFFu, mb = sm >> 16;
-        const bool fast = w4a16_single_rounding_exact(sb, mb);
-        const uint4 w0 = w4a16_dequant8(c.x, sb, mb, fast);   // elements [8q, 8q+8)
-        const uint4 w1 = w4a16_dequant8(c.y, sb, mb, fast);   // elements [32+8q, 32+8q+8)
-        const uint32_t ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-        for (int r = 0; r < MR; ++r) {
-            if (r < m) {
-                const uint16_t *xr = x + static_cast<size_t>(r) * k + g * 64 + 8 * q;
-                const uint4 x0 = *reinterpret_cast<const uint4 *>(xr);
-                const uint4 x1 = *reinterpret_cast<const uint4 *>(xr + 32);
-                const uint32_t xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    acc[r] = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2h, ws[e]), __builtin_bit_cast(v2h, xs[e]),
-                                                    acc[r], false);
+        for (int u = 0; u < GEMV_BATCH; ++u) {
+            if (g + u < g_end) {
+                const v2u t =
+                    __builtin_nontemporal_load(reinterpret_cast<const v2u *>(cp + static_cast<size_t>(g + u) * 512));
+                c[b][u] = uint2{t[0], t[1]};
+                sm[b][u] = __builtin_nontemporal_load(sp + static_cast<size_t>(g + u) * 16);
             }
         }
     };
+    load_batch(0, g_begin);
+    load_batch(1, g_begin + GEMV_BATCH);
 
-    int g = wave;
-    for (; g + (GEMV_UNROLL - 1) * GEMV_WAVES < groups; g += GEMV_UNROLL * GEMV_WAVES) {
-        uint2 c[GEMV_UNROLL];
-        uint32_t sm[GEMV_UNROLL];
-#pragma unroll
-        for (int u = 0; u < GEMV_UNROLL; ++u) {
-            const int gg = g + u * GEMV_WAVES;
-            c[u] = *reinterpret_cast<const uint2 *>(cp + static_cast<size_t>(gg) * 512);
-            sm[u] = sp[static_cast<size_t>(gg) * 16];
-        }
-#pragma unroll
-        for (int u = 0; u < GEMV_UNROLL; ++u) consume(g + u * GEMV_WAVES, c[u], sm[u]);
+    if (XLDS) {
+        const int chunks = m * k / 8;  // 16-byte chunks
+        for (int i = threadIdx.x; i < chunks; i += GEMV_WAVES * WAVE)
+            reinterpret_cast<uint4 *>(xs_lds)[i] = reinterpret_cast<const uint4 *>(x)[i];
     }
-    for (; g < groups; g += GEMV_WAVES) {
-        const uint2 c = *reinterpret_cast<const uint2 *>(cp + static_cast<size_t>(g) * 512);
-        consume(g, c, sp[static_cast<size_t>(g) * 16]);
+    // The matrix-core B operand: lane l supplies row m = l % 16 of x, inputs
+    // 8q .. 8q + 7 of each 32-wide half group.  Lanes past the last row read
+    // row 0: they only feed output columns that are never stored.
+    const uint16_t *xrow = (XLDS ? xs_lds : x) + static_cast<size_t>(r16 < m ? r16 : 0) * k + 8 * q;
+    if (XLDS) __syncthreads();
+
+    // acc[r] = y[m = l % 16][n = 16 tile + 4 (l / 16) + r] over this wave's
+    // groups (16x16 accumulator layout, A = weights, B = x).
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    auto consume = [&](int g, uint2 cc, uint32_t smm) {
+        const uint32_t sb = smm & 0xFFFFu, mb = smm >> 16;
+        // Wave-uniform, so a wave runs one dequantisation form, not both.
+        const bool fast = __all(w4a16_single_rounding_exact(sb, mb));
+        const uint4 w0 = w4a16_dequant8(cc.x, sb, mb, fast);   // elements [8q, 8q+8)
+        const uint4 w1 = w4a16_dequant8(cc.y, sb, mb, fast);   // elements [32+8q, 32+8q+8)
+        const uint4 x0 = *reinterpret_cast<const uint4 *>(xrow + g * 64);
+        const uint4 x1 = *reinterpret_cast<const uint4 *>(xrow + g * 64 + 32);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, w0), __builtin_bit_cast(v8h, x0), acc, 0,
+                                                     0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, w1), __builtin_bit_cast(v8h, x1), acc, 0,
+                                                     0, 0);
+    };
+    for (int g = g_begin; g < g_end; g += 2 * GEMV_BATCH) {
+#pragma unroll
+        for (int u = 0; u < GEMV_BATCH; ++u)
+            if (g + u < g_end) consume(g + u, c[0][u], sm[0][u]);
+        load_batch(0, g + 2 * GEMV_BATCH);
+#pragma unroll
+        for (int u = 0; u < GEMV_BATCH; ++u)
+            if (g + GEMV_BATCH + u < g_end) consume(g + GEMV_BATCH + u, c[1][u], sm[1][u]);
+        load_batch(1, g + 3 * GEMV_BATCH);
     }
 
 #pragma unroll
-    for (int r = 0; r < MR; ++r) {
-        const float v = wave_sum16(acc[r]);
-        if (q == 0) partial[wave][r][r16] = v;
-    }
+    for (int r = 0; r < 4; ++r) partial[wave][4 * q + r][r16] = acc[r];
     __syncthreads();
-    if (wave == 0 && lane < 16) {
-        const int col = tile * 16 + lane;
+    // Thread t (of the first 256) finishes output n = t / 16 of row m = t % 16.
+    {
+        const int t = threadIdx.x, nn = t >> 4, mm = t & 15;
+        if (mm < m) {
+            float v = partial[0][nn][mm];
 #pragma unroll
-        for (int r = 0; r < MR; ++r) {
-            if (r < m) {
-                float v = partial[0][r][lane];
+            for (int w = 1; w < GEMV_WAVES; ++w) v += partial[w][nn][mm];
+            const int col = tile * 16 + nn;
+            store_out(y, static_cast<size_t>(mm) * n + col, epilogue(v, bias, col, epi), out_type);
+        }
+    }
+}
+
+// Factored form, used when x fits in LDS.  Per group g and output n:
+//   y += s (P - 1024 X) + min X,  P = sum_k x_k (1024 + c_k),  X = sum_k x_k
+// The codes enter the matrix core as the exact fp16 integers 1024 + c (a
+// bit-field insert into 0x6400, no multiply), P is exact per product and
+// summed in fp32, and X is summed once per workgroup from the staged rows.
+// This is the group's dot product with the weights c s + min kept in fp32,
+// instead of first rounding every weight to fp16 as the reference's
+// dequantiser does (gemm.cu:229-230): the outputs differ from that form by
+// the fp16 weight rounding only, well inside the W4A16 output tolerance.
+__global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_factored_kernel(
+    const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
+    const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int m, int n, int k) {
+    __shared__ float partial[GEMV_WAVES][16][17];
+    extern __shared__ __attribute__((aligned(16))) uint16_t xs_lds[];  // m * k fp16, then m * G fp32 sums
+    const int groups = k >> 6;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
+    const int q = lane >> 4, r16 = lane & 15;
+    const int tile = blockIdx.x;
+    float *xsum = reinterpret_cast<float *>(xs_lds + static_cast<size_t>(m) * k);
+
+    const int per_wave = (groups + GEMV_WAVES - 1) / GEMV_WAVES;
+    const int g_begin = wave * per_wave;
+    const int g_end = min(groups, g_begin + per_wave);
+    const uint8_t *cp = codes + static_cast<size_t>(tile) * groups * 512 + lane * 8;
+    // The (scale, minimum) pairs of this lane's four outputs 4q .. 4q+3.
+    const uint8_t *sp = reinterpret_cast<const uint8_t *>(scales) + static_cast<size_t>(tile) * groups * 64 + q * 16;
+
+    uint2 c[2][GEMV_BATCH];
+    uint4 sc[2][GEMV_BATCH];
+    auto load_batch = [&](int b, int g) {
 #pragma unroll
-                for (int w = 1; w < GEMV_WAVES; ++w) v += partial[w][r][lane];
-                store_out(y, static_cast<size_t>(r) * n + col, epilogue(v, bias, col, epi), out_type);
+        for (int u = 0; u < GEMV_BATCH; ++u) {
+            if (g + u < g_end) {
+                const v2u t =
+                    __builtin_nontemporal_load(reinterpret_cast<const v2u *>(cp + static_cast<size_t>(g + u) * 512));
+                c[b][u] = uint2{t[0], t[1]};
+                const v4u v =
+                    __builtin_nontemporal_load(reinterpret_cast<const v4u *>(sp + static_cast<size_t>(g + u) * 64));
+                sc[b][u] = uint4{v[0], v[1], v[2], v[3]};
             }
         }
+    };
+    load_batch(0, g_begin);
+    load_batch(1, g_begin + GEMV_BATCH);
+
+    const int chunks = m * k / 8;  // 16-byte chunks of x
+    for (int i = threadIdx.x; i < chunks; i += GEMV_WAVES * WAVE)
+        reinterpret_cast<uint4 *>(xs_lds)[i] = reinterpret_cast<const uint4 *>(x)[i];
+    __syncthreads();
+    for (int i = threadIdx.x; i < m * groups; i += GEMV_WAVES * WAVE) {
+        const uint16_t *src = xs_lds + static_cast<size_t>(i) * 64;  // row i / G, group i % G
+        float t = 0.f;
+#pragma unroll 8
+        for (int e = 0; e < 64; ++e) t += h2f(src[e]);
+        xsum[i] = t;
     }
+    __syncthreads();
+
+    // B operand: lane l supplies row m = l % 16 of x, inputs 8q .. 8q + 7 of
+    // each 32-wide half group.  Lanes past the last row read row 0: they only
+    // feed output columns that are never stored.
+    const int xr = r16 < m ? r16 : 0;
+    const uint16_t *xrow = xs_lds + static_cast<size_t>(xr) * k + 8 * q;
+    const float *xs_row = xsum + static_cast<size_t>(xr) * groups;
+    uint32_t magic = 0x64006400u;
+    asm volatile("" : "+v"(magic));  // kept in a VGPR: lets the insert be one v_bfi_b32
+
+    // yacc[r] = y[m = l % 16][n = 16 tile + 4q + r] over this wave's groups.
+    float yacc[4] = {0.f, 0.f, 0.f, 0.f};
+    auto consume = [&](int g, uint2 cc, uint4 scs) {
+        // Bit-field insert of each nibble pair into 0x6400 (written in C, not
+        // inline asm: these values feed the matrix core directly, and only
+        // compiler-visible instructions get the VALU-to-MFMA wait states).
+        uint32_t a[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            a[i] = ((cc.x >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu);
+            a[4 + i] = ((cc.y >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu);
+        }
+        const uint4 x0 = *reinterpret_cast<const uint4 *>(xrow + g * 64);
+        const uint4 x1 = *reinterpret_cast<const uint4 *>(xrow + g * 64 + 32);
+        // The nibble slot order of the tiled codes puts element 2i in nibble
+        // i and 2i+1 in nibble 4+i, so a[i] holds elements (2i, 2i+1).
+        v4f p = {0.f, 0.f, 0.f, 0.f};
+        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, uint4{a[0], a[1], a[2], a[3]}),
+                                                   __builtin_bit_cast(v8h, x0), p, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, uint4{a[4], a[5], a[6], a[7]}),
+                                                   __builtin_bit_cast(v8h, x1), p, 0, 0, 0);
+        const float X = xs_row[g];
+        const uint32_t sm4[4] = {scs.x, scs.y, scs.z, scs.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float t = __builtin_fmaf(-1024.0f, X, p[r]);
+            yacc[r] = __builtin_fmaf(h2f(static_cast<uint16_t>(sm4[r] & 0xFFFFu)), t, yacc[r]);
+            yacc[r] = __builtin_fmaf(h2f(static_cast<uint16_t>(sm4[r] >> 16)), X, yacc[r]);
+        }
+    };
+    for (int g = g_begin; g < g_end; g += 2 * GEMV_BATCH) {
+#pragma unroll
+        for (int u = 0; u < GEMV_BATCH; ++u)
+            if (g + u < g_end) consume(g + u, c[0][u], sc[0][u]);
+        load_batch(0, g + 2 * GEMV_BATCH);
+#pragma unroll
+        for (int u = 0; u < GEMV_BATCH; ++u)
+            if (g + GEMV_BATCH + u < g_end) consume(g + GEMV_BATCH + u, c[1][u], sc[1][u]);
+        load_batch(1, g + 3 * GEMV_BATCH);
+    }
+
+#pragma unroll
+    for (int r = 0; r < 4; ++r) partial[wave][4 * q + r][r16] = yacc[r];
+    __syncthreads();
+    {
+        const int t = threadIdx.x, nn = t >> 4, mm = t & 15;
+        if (mm < m) {
+            float v = partial[0][nn][mm];
+#pragma unroll
+            for (int w = 1; w < GEMV_WAVES; ++w) v += partial[w][nn][mm];
+            const int col = tile * 16 + nn;
+            store_out(y, static_cast<size_t>(mm) * n + col, epilogue(v, bias, col, epi), out_type);
+        }
+    }
+}
+
+static void launch_gemv(const uint16_t *x, const uint8_t *c, const uint16_t *s, const float *bias, void *y,
+                        int out_type, int epi, int m, int n, int k, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(n / 16)), block(GEMV_WAVES * WAVE);
+    const long long lds = static_cast<long long>(m) * k * 2 + static_cast<long long>(m) * (k / 64) * 4;
+    if (lds <= GEMV_LDS_X)
+        w4a16_gemv_factored_kernel<<<grid, block, static_cast<size_t>(lds), stream>>>(x, c, s, bias, y, out_type, epi,
+                                                                                      m, n, k);
+    else
+        w4a16_gemv_kernel<false><<<grid, block, 0, stream>>>(x, c, s, bias, y, out_type, epi, m, n, k);
 }
 
 }  // namespace qi
@@ -105,20 +265,10 @@ using namespace qi;
 int qi_hip_w4a16_gemv_impl(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
                            const float *bias, void *y, int out_type, int epilogue, int m, int n, int k,
                            hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>(n / 16)), block(GEMV_WAVES * WAVE);
     const uint16_t *x = static_cast<const uint16_t *>(x_half);
     const uint8_t *c = static_cast<const uint8_t *>(w_tiled_codes);
     const uint16_t *s = static_cast<const uint16_t *>(w_tiled_scales);
-    if (m <= 1)
-        w4a16_gemv_kernel<1><<<grid, block, 0, stream>>>(x, c, s, bias, y, out_type, epilogue, m, n, k);
-    else if (m <= 2)
-        w4a16_gemv_kernel<2><<<grid, block, 0, stream>>>(x, c, s, bias, y, out_type, epilogue, m, n, k);
-    else if (m <= 4)
-        w4a16_gemv_kernel<4><<<grid, block, 0, stream>>>(x, c, s, bias, y, out_type, epilogue, m, n, k);
-    else if (m <= 8)
-        w4a16_gemv_kernel<8><<<grid, block, 0, stream>>>(x, c, s, bias, y, out_type, epilogue, m, n, k);
-    else
-        w4a16_gemv_kernel<16><<<grid, block, 0, stream>>>(x, c, s, bias, y, out_type, epilogue, m, n, k);
+    launch_gemv(x, c, s, bias, y, out_type, epilogue, m, n, k, stream);
     return launch_status();
 }
 

@@ -89,9 +89,14 @@ __device__ __forceinline__ uint4 w4a16_dequant8(uint32_t x, uint32_t scale_bits,
         const v2h s2 = __builtin_bit_cast(v2h, scale_bits | (scale_bits << 16));
         const v2h m2 = __builtin_bit_cast(v2h, minimum_bits | (minimum_bits << 16));
         const v2h k1024 = v2h{static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+        uint32_t magic = 0x64006400u;
+        asm volatile("" : "+v"(magic));
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const v2h c = __builtin_bit_cast(v2h, ((x >> (4 * i)) & 0x000F000Fu) | 0x64006400u) - k1024;
+            // Nibble pair -> fp16 1024 + c: one and-or with the 0x6400
+            // pattern held in a VGPR.
+            const uint32_t biased = ((x >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu);
+            const v2h c = __builtin_bit_cast(v2h, biased) - k1024;
             out[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, s2, m2));
         }
     } else {

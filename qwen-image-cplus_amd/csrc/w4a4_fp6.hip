@@ -26,12 +26,14 @@
 // holds y[m = l % 32][n = 8a + 4 * (l / 32) + r]: four consecutive outputs,
 // stored with one wide write.
 //
-// Pipeline.  A ring of NSTAGE LDS slots holds the operand blocks of upcoming
-// groups, filled NSTAGE-1 groups ahead by 12-byte-per-lane
-// buffer_load ... lds (one instruction per 768-byte half block; the data
-// lands at a 16-byte lane pitch); the scales ride in a register ring.  One
-// barrier per group.
+// Pipeline.  A ring of NSTAGE LDS slots holds the operand and scale blocks
+// of upcoming groups, filled NSTAGE-1 groups ahead by buffer_load ... lds
+// (12 bytes per lane for operands: one instruction per 768-byte half block,
+// landing at a 16-byte lane pitch; 4 bytes per lane for scales).  One barrier
+// per group; each group's matrix-core work is issued before the barrier and
+// the next group's LDS reads overlap its fp32 step.
 
+#include <cstdlib>
 #include <utility>
 
 #include "qi_common.h"
@@ -91,7 +93,7 @@ __device__ __forceinline__ v8i fp6_operand(v3i lo, v3i hi) {
 }
 
 template <int TM, int TN, int WM, int WN, int NSTAGE>
-__global__ __launch_bounds__(WM *WN *WAVE, 2) void w4a4_fp6_kernel(
+__global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2))) void w4a4_fp6_kernel(
     const uint8_t *__restrict__ a6, const uint16_t *__restrict__ sa_t, const uint8_t *__restrict__ w6,
     const uint16_t *__restrict__ sw_t, const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi,
     int m, int n, int k) {
@@ -101,12 +103,11 @@ __global__ __launch_bounds__(WM *WN *WAVE, 2) void w4a4_fp6_kernel(
     constexpr int HALVES = 2 * (MT + NTL);      // 768-byte loads per group
     static_assert(HALVES % NW == 0, "loader mapping");
     constexpr int L_PER_W = HALVES / NW;
-    static_assert((2 * MT) % L_PER_W == 0, "a wave's loads come from one operand");
-    static_assert(TM <= 4 && TN == 2, "one scale load per operand per wave; scale products pair the n-tiles");
+    static_assert(TM <= 4 && TN <= 2, "one scale load per operand per wave; scale products pair the n-tiles");
     constexpr int LOADS_PER_GROUP = L_PER_W + 2;  // per wave: operands + sa + sw
     constexpr int TILE = 2048, SLOT = (MT + NTL) * TILE;
     constexpr int SC_WAVE = 512, SC_SLOT = NW * SC_WAVE;  // scale bytes per wave / per slot
-    static_assert(NSTAGE * SLOT <= 65536 && NSTAGE * SC_SLOT <= 65536, "LDS offsets");
+    static_assert(NSTAGE * (SLOT + SC_SLOT) <= 160 * 1024, "LDS size");
     __shared__ __attribute__((aligned(16))) uint8_t lds[NSTAGE * SLOT];
     __shared__ __attribute__((aligned(16))) uint8_t lds_sc[NSTAGE * SC_SLOT];
 
@@ -132,12 +133,11 @@ __global__ __launch_bounds__(WM *WN *WAVE, 2) void w4a4_fp6_kernel(
     // block's (MT + NTL) tiles, activation tiles first.  Missing tiles read
     // past the buffer end, which returns zeros.
     const int H0 = wave * L_PER_W;
-    const bool from_a = H0 < 2 * MT;
-    const v4i_rsrc rsrc = from_a ? ra : rw;
     uint32_t vo[L_PER_W];
 #pragma unroll
     for (int u = 0; u < L_PER_W; ++u) {
         const int H = H0 + u, X = H >> 1, half = H & 1;
+        const bool from_a = H < 2 * MT;
         const int t = from_a ? mt0 + X : nt0 + X - MT;
         const bool ok = from_a ? t < m_tiles : t < n_tiles;
         vo[u] = ok ? static_cast<uint32_t>(t) * groups * 1536u + half * 768u + lane * 12u
@@ -161,7 +161,7 @@ __global__ __launch_bounds__(WM *WN *WAVE, 2) void w4a4_fp6_kernel(
 #pragma unroll
         for (int u = 0; u < L_PER_W; ++u) {
             const int H = H0 + u;
-            dma_dwordx3(rsrc, lds0 + slot * SLOT + (H >> 1) * TILE + (H & 1) * 1024, vo[u], g * 1536);
+            dma_dwordx3(H < 2 * MT ? ra : rw, lds0 + slot * SLOT + (H >> 1) * TILE + (H & 1) * 1024, vo[u], g * 1536);
         }
         dma_dword(rsa, sc0 + slot * SC_SLOT + wave * SC_WAVE, sa_vo, g * 64);
         dma_dword(rsw, sc0 + slot * SC_SLOT + wave * SC_WAVE + 256, sw_vo, g * 64);
@@ -185,38 +185,42 @@ __global__ __launch_bounds__(WM *WN *WAVE, 2) void w4a4_fp6_kernel(
     const uint8_t *sa_lds = lds_sc + wave * SC_WAVE + r32 * 2;
     const uint8_t *sw_lds = lds_sc + wave * SC_WAVE + 256 + lane * 2;
 
-    auto compute = [&](auto slot_c) {
-        constexpr int slot = decltype(slot_c)::value;
+    struct Frags {  // raw LDS reads; converted where consumed
         v8i wf[TN], xf[TM];
-        float sal[TM];
+        uint32_t sal[TM], swl;
+    };
+    auto read_frags = [&](auto slot_c, Frags &F) {
+        constexpr int slot = decltype(slot_c)::value;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             const v3i lo = *reinterpret_cast<const v3i *>(w_frag + slot * SLOT + j * TILE);
             const v3i hi = *reinterpret_cast<const v3i *>(w_frag + slot * SLOT + j * TILE + 1024);
-            wf[j] = fp6_operand(lo, hi);
+            F.wf[j] = fp6_operand(lo, hi);
         }
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             const v3i lo = *reinterpret_cast<const v3i *>(x_frag + slot * SLOT + i * TILE);
             const v3i hi = *reinterpret_cast<const v3i *>(x_frag + slot * SLOT + i * TILE + 1024);
-            xf[i] = fp6_operand(lo, hi);
-            sal[i] = h2f(*reinterpret_cast<const uint16_t *>(sa_lds + slot * SC_SLOT + 64 * i));
+            F.xf[i] = fp6_operand(lo, hi);
+            F.sal[i] = *reinterpret_cast<const uint16_t *>(sa_lds + slot * SC_SLOT + 64 * i);
         }
-        const float swl = h2f(*reinterpret_cast<const uint16_t *>(sw_lds + slot * SC_SLOT));
-        // All matrix-core work of the group first (scale outer products,
-        // then the four partial tiles), so the matrix core runs while the
-        // fp32 steps of earlier tiles execute.  Block b of the 32x32x1 outer
-        // product has rows = outputs of n-tile b (lanes 32b .. 32b+31 supply
-        // them) and columns = rows m of tile i; its result registers
-        // 16b .. 16b+15 line up with the accumulator registers.
-        v32f sp[TM];
-        v16f p[TN][TM];
+        F.swl = *reinterpret_cast<const uint16_t *>(sw_lds + slot * SC_SLOT);
+    };
+    // Matrix-core work of one group: the scale outer products and the
+    // partial tiles.  Block b of the 32x32x1 outer product has rows = outputs
+    // of n-tile b (lanes 32b .. 32b+31 supply them) and columns = rows m of
+    // tile i; its result registers 16b .. 16b+15 line up with the
+    // accumulator registers.
+    v32f sp[TM];
+    v16f p[TN][TM];
+    auto mfma = [&](const Frags &F) {
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             v32f z32;
 #pragma unroll
             for (int r = 0; r < 32; ++r) z32[r] = 0.f;
-            sp[i] = __builtin_amdgcn_mfma_f32_32x32x1f32(swl, sal[i], z32, 0, 0, 0);
+            sp[i] = __builtin_amdgcn_mfma_f32_32x32x1f32(h2f(static_cast<uint16_t>(F.swl)),
+                                                         h2f(static_cast<uint16_t>(F.sal[i])), z32, 0, 0, 0);
         }
 #pragma unroll
         for (int j = 0; j < TN; ++j)
@@ -226,8 +230,11 @@ __global__ __launch_bounds__(WM *WN *WAVE, 2) void w4a4_fp6_kernel(
 #pragma unroll
                 for (int r = 0; r < 16; ++r) z[r] = 0.f;
                 // fmt 2 = FP6 E2M3 for both operands; block scales 2^0.
-                p[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[j], xf[i], z, 2, 2, 0, 127, 0, 127);
+                p[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(F.wf[j], F.xf[i], z, 2, 2, 0, 127, 0, 127);
             }
+    };
+    // The exact fp32 step of one group, in ascending group order.
+    auto fmas = [&]() {
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
@@ -236,24 +243,50 @@ __global__ __launch_bounds__(WM *WN *WAVE, 2) void w4a4_fp6_kernel(
                 for (int r = 0; r < 16; ++r) acc[j][i][r] = __builtin_fmaf(p[j][i][r], sp[i][16 * j + r], acc[j][i][r]);
     };
 
-    // Prologue; loads past the last group read harmless bytes into slots
-    // that are never consumed and keep the loads per group constant.
+    // Software pipeline, per group g (slots are g mod NSTAGE):
+    //   matrix-core work of g (fragments read during g - 1);
+    //   wait until this wave's loads of g + 1 are done, barrier (then every
+    //   wave's are, and every wave has consumed its reads of slot g - 1);
+    //   issue the loads of g + NSTAGE - 1 into slot g - 1;
+    //   read the fragments of g + 1, which land during
+    //   the fp32 step of g.
+    // Loads past the last group read harmless bytes into slots that are
+    // never consumed and keep the loads per group constant.
+    static_assert(NSTAGE % 4 == 0, "whole quarters of the ring per group count (groups % 4 == 0)");
+    Frags F[2];
 #pragma unroll
-    for (int p = 0; p < NSTAGE - 1; ++p) issue(p, p);
+    for (int q = 0; q < NSTAGE - 1; ++q) issue(q, q);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTAGE - 2) * LOADS_PER_GROUP) : "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    read_frags(std::integral_constant<int, 0>{}, F[0]);
     for (int g0 = 0; g0 < groups; g0 += NSTAGE) {
         static_for<NSTAGE>([&](auto uc) {
             constexpr int u = decltype(uc)::value;
             const int g = g0 + u;
-            // This wave's loads of group g are done; after the barrier so are
-            // every wave's, and every wave has finished reading the slot the
-            // next issue overwrites (compute ends with lgkmcnt(0)).  A bare
-            // s_barrier: __syncthreads' release fence would also wait for
-            // the loads of the groups still in flight.
-            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((NSTAGE - 2) * LOADS_PER_GROUP) : "memory");
-            __builtin_amdgcn_s_barrier();
-            asm volatile("" ::: "memory");
-            issue(g + NSTAGE - 1, (u + NSTAGE - 1) % NSTAGE);
-            if (g < groups) compute(uc);
+            // groups is a multiple of 4, so only whole quarters of a
+            // NSTAGE = 8 ring can be missing at the end; the test is uniform
+            // and covers a whole iteration, so no partial tile stays live
+            // across iterations.  After the last group the reads of group
+            // `groups` fetch harmless slot contents that are never used.
+            if (u < 4 || g < groups) {
+                // Scheduling fences pin the phase order: the compiler would
+                // otherwise sink the matrix-core work below the barrier and
+                // the next group's reads, and wait for those reads.
+                __builtin_amdgcn_sched_barrier(0);
+                mfma(F[u & 1]);
+                __builtin_amdgcn_sched_barrier(0);
+                // A bare s_barrier: __syncthreads' release fence would also
+                // wait for the loads of the groups still in flight.
+                asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((NSTAGE - 3) * LOADS_PER_GROUP) : "memory");
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                issue(g + NSTAGE - 1, (u + NSTAGE - 1) % NSTAGE);
+                read_frags(std::integral_constant<int, (u + 1) % NSTAGE>{}, F[(u + 1) & 1]);
+                __builtin_amdgcn_sched_barrier(0);
+                fmas();
+                __builtin_amdgcn_sched_barrier(0);
+            }
         });
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -320,6 +353,39 @@ QI_API int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *a_scales_tiled
         static_cast<long long>(n / 32) * g * 1536 >= (1LL << 31))
         return kInvalid;
     hipStream_t s = stream_of(stream);
-    return launch_fp6<2, 2, 2, 2, 4>(a_codes6, a_scales_tiled, w_codes6, w_scales_tiled, bias, y, out_type, epilogue,
-                                     m, n, k, s);
+    // Tile shapes (measured on MI355X): 128 x 128 with four waves when that
+    // already gives two workgroups per CU; otherwise, for short M, single-
+    // wave 32 x 32 tiles with an 8-deep ring, or 64 x 128 four-wave tiles
+    // when N is wide.  QI_HIP_FP6_TILES (0..4) overrides the choice, for
+    // tuning.
+    static const int forced = [] {
+        const char *e = getenv("QI_HIP_FP6_TILES");
+        return e ? atoi(e) : -1;
+    }();
+    int cfg;
+    if (static_cast<long long>((m + 127) / 128) * ((n + 127) / 128) >= 512)
+        cfg = 0;
+    else
+        cfg = n >= 8192 ? 3 : 4;
+    if (forced >= 0) cfg = forced;
+    switch (cfg) {
+    case 0:
+        return launch_fp6<2, 2, 2, 2, 4>(a_codes6, a_scales_tiled, w_codes6, w_scales_tiled, bias, y, out_type,
+                                         epilogue, m, n, k, s);
+    case 1:
+        return launch_fp6<1, 2, 1, 1, 8>(a_codes6, a_scales_tiled, w_codes6, w_scales_tiled, bias, y, out_type,
+                                         epilogue, m, n, k, s);
+    case 2:
+        return launch_fp6<2, 2, 1, 1, 8>(a_codes6, a_scales_tiled, w_codes6, w_scales_tiled, bias, y, out_type,
+                                         epilogue, m, n, k, s);
+    case 3:
+        return launch_fp6<1, 2, 2, 2, 4>(a_codes6, a_scales_tiled, w_codes6, w_scales_tiled, bias, y, out_type,
+                                         epilogue, m, n, k, s);
+    case 4:
+        return launch_fp6<1, 1, 1, 1, 8>(a_codes6, a_scales_tiled, w_codes6, w_scales_tiled, bias, y, out_type,
+                                         epilogue, m, n, k, s);
+    default:
+        return launch_fp6<2, 2, 2, 2, 4>(a_codes6, a_scales_tiled, w_codes6, w_scales_tiled, bias, y, out_type,
+                                         epilogue, m, n, k, s);
+    }
 }

@@ -83,8 +83,11 @@ def test_fp6_weight_relayout(dev):
     np.testing.assert_array_equal(_u16(ts).reshape(n, k // 64), tiled_scales(s, n))
 
 
+# Shapes cover every tile configuration the dispatcher picks: single-wave
+# 32 x 32 tiles (short M), 64 x 128 tiles (short M, N >= 8192) and 128 x 128
+# tiles (at least 512 of them).
 @pytest.mark.parametrize("m,n,k", [(1, 32, 256), (5, 96, 512), (100, 256, 768), (263, 128, 1024),
-                                   (640, 1024, 512), (1024, 512, 3072)])
+                                   (640, 1024, 512), (1024, 512, 3072), (100, 8192, 512), (2048, 4096, 256)])
 def test_fp6_gemm_bit_exact(dev, m, n, k):
     print(f"fp6 gemm m={m} n={n} k={k}", flush=True)
     import qwen_image_hip.ops as ops

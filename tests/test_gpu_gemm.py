@@ -247,4 +247,10 @@ def test_w4a16_dequant_bit_exact_identity(dev, path):
         else:
             got = np.concatenate([ops.w4a16_gemv(_dev(eye[r:r + 16], dev), tc, ts).cpu().numpy()
                                   for r in range(0, k, 16)], axis=0).T
+            # The GEMV keeps each weight c * s + minimum in fp32 (one
+            # rounding of the exact value) instead of rounding it to fp16.
+            nib = np.stack([codes & 15, codes >> 4], -1).reshape(n, k).astype(np.float64)
+            s64 = np.repeat(scales.view(np.float16).astype(np.float64), 64, axis=1)
+            m64 = np.repeat(mins.view(np.float16).astype(np.float64), 64, axis=1)
+            want = (nib * s64 + m64).astype(np.float32)
     np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
