@@ -107,6 +107,10 @@ class StepW4A4:
                 "h": torch.empty((m, MLP), dtype=torch.float16, device="cuda"),
             }
 
+    def outputs(self):
+        """Copies of the buffers the step writes last (per stream: MLP hidden h, down output y)."""
+        return [self.bufs[st][name].clone() for st in STREAMS for name in ("h", "y")]
+
     def __call__(self):
         import torch
 
@@ -302,6 +306,7 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="only the headline W4A4 block")
+    ap.add_argument("--no-graph", action="store_true", help="time the eager step (one Python call per linear)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="run only the dominant GEMM (20 launches) and a 512 MiB device copy (5 launches), "
                          "for hardware-counter runs")
@@ -321,20 +326,49 @@ def main(argv=None) -> int:
     log("packing W4A4 block weights (fp6 operands)")
     blk4 = Block(q.SCHEME_W4A4_H256, 1)
     step4 = StepW4A4(blk4, 2)
+
+    # Eager: one Python call per linear.
+    ms_eager = time_fn(step4, args.steps, args.warmup)
+    eager_out = step4.outputs()
+
+    # Graph: the step's 20 launches captured once into a HIP graph and
+    # replayed, as a serving loop would, so the host's per-launch cost is not
+    # on the GPU's critical path.  Every replay must reproduce the eager
+    # outputs bit for bit.
+    graph = None
+    if not args.no_graph:
+        capture = torch.cuda.Stream()
+        capture.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(capture):
+            step4()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=capture):
+            step4()
+        torch.cuda.synchronize()
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            for a, b in zip(eager_out, step4.outputs()):
+                if not torch.equal(a, b):
+                    raise RuntimeError("graph replay differs from the eager step")
+    run = graph.replay if graph is not None else step4
     for _ in range(args.warmup):
-        step4()
+        run()
     torch.cuda.synchronize()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record()
     for _ in range(args.steps):
-        step4()
+        run()
     stop.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = start.elapsed_time(stop) / args.steps
     tops = block_ops() / (ms_step * 1e-3) / 1e12
-    log(f"w4a4 block: {ms_step:.3f} ms/step, {tops:.1f} TOPS (wall {wall:.3f} s)")
+    log(f"w4a4 block: {ms_step:.3f} ms/step ({'graph' if graph else 'eager'}), {tops:.1f} TOPS "
+        f"(wall {wall:.3f} s); eager {ms_eager:.3f} ms/step")
+    del graph
 
     dom_ms, dom_ops = dominant_kernel(blk4, step4)
     achieved = dom_ops / (dom_ms * 1e-3) / 1e12
@@ -379,7 +413,7 @@ def main(argv=None) -> int:
     line = {
         "metric": "QIPACK W4A4/W4A16 linear TOPS + % roofline, MMDiT block @1024^2 (M=4352)",
         "value": round(tops, 2), "unit": "TOPS", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "ms_per_step": round(ms_step, 4), "ms_per_step_eager": round(ms_eager, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int4 x int4 exact group partials (fp6 E2M3 MFMA operands), fp32 epilogue, fp16 out", "data": "synthetic",
         "config": {"workload": "W4A4 H256 g64 one MMDiT dual-stream block linears (config 3): image M=4096 + "
                                "text M=256, hidden 3072, MLP 12288, heavy-tailed fp16 activations, online quantiser",
