@@ -88,8 +88,10 @@ __device__ __forceinline__ void static_for(F &&f) {
 }
 
 // The MFMA reads six dwords of an fp6 operand; the last two are don't-care.
-__device__ __forceinline__ v8i fp6_operand(v3i lo, v3i hi) {
-    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, -1, -1);
+// Each half is read as a full 16-byte slot (ds_read_b128 runs at twice the
+// rate of ds_read_b96 on gfx950); its fourth dword is padding.
+__device__ __forceinline__ v8i fp6_operand(v4i lo, v4i hi) {
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 4, 5, 6, -1, -1);
 }
 
 template <int TM, int TN, int WM, int WN, int NSTAGE>
@@ -193,14 +195,14 @@ __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2)
         constexpr int slot = decltype(slot_c)::value;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const v3i lo = *reinterpret_cast<const v3i *>(w_frag + slot * SLOT + j * TILE);
-            const v3i hi = *reinterpret_cast<const v3i *>(w_frag + slot * SLOT + j * TILE + 1024);
+            const v4i lo = *reinterpret_cast<const v4i *>(w_frag + slot * SLOT + j * TILE);
+            const v4i hi = *reinterpret_cast<const v4i *>(w_frag + slot * SLOT + j * TILE + 1024);
             F.wf[j] = fp6_operand(lo, hi);
         }
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
-            const v3i lo = *reinterpret_cast<const v3i *>(x_frag + slot * SLOT + i * TILE);
-            const v3i hi = *reinterpret_cast<const v3i *>(x_frag + slot * SLOT + i * TILE + 1024);
+            const v4i lo = *reinterpret_cast<const v4i *>(x_frag + slot * SLOT + i * TILE);
+            const v4i hi = *reinterpret_cast<const v4i *>(x_frag + slot * SLOT + i * TILE + 1024);
             F.xf[i] = fp6_operand(lo, hi);
             F.sal[i] = *reinterpret_cast<const uint16_t *>(sa_lds + slot * SC_SLOT + 64 * i);
         }
