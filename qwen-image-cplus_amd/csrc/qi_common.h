@@ -14,6 +14,10 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
+// The direct-to-LDS loads below set M0 inside inline asm; nothing else in
+// these kernels uses it, so the clobber warning does not apply.
+#pragma clang diagnostic ignored "-Winline-asm"
+
 namespace qi {
 
 constexpr int GROUP = 64;      // QIPACK v6 group size along K
@@ -145,6 +149,44 @@ __device__ __forceinline__ uint32_t int4_to_e2m3(int q) {
     const uint32_t a = static_cast<uint32_t>(q < 0 ? -q : q);
     const uint32_t code = a == 0 ? 0u : (a == 1 ? 8u : (a < 4 ? 16u + 4u * (a - 2) : 24u + 2u * (a - 4)));
     return (q < 0 ? 32u : 0u) | code;
+}
+
+typedef int v4i_rsrc __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource (base, size in bytes; loads past the end return zero)
+// as four scalar dwords for the inline loads below.
+__device__ __forceinline__ v4i_rsrc raw_rsrc(const void *p, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    return v4i_rsrc{static_cast<int>(a), static_cast<int>((a >> 32) & 0xFFFF), static_cast<int>(bytes), 0x00020000};
+}
+
+// Direct-to-LDS buffer loads, written as inline asm so the compiler does not
+// track them: it would otherwise make every LDS read and every barrier wait
+// for all of them, including the loads of later groups into other slots.
+// Their completion is counted explicitly with s_waitcnt vmcnt.  Lane i's
+// data lands at lds_addr + 16 i (12- and 16-byte forms) or + 4 i (4-byte
+// form).
+// Nothing else in these kernels uses M0.
+__device__ __forceinline__ void dma_dwordx3(v4i_rsrc rsrc, uint32_t lds_addr, uint32_t voffset, uint32_t soffset) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx3 %1, %2, %3 offen lds" ::"s"(lds_addr),
+                 "v"(voffset), "s"(rsrc), "s"(soffset)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ void dma_dwordx4(v4i_rsrc rsrc, uint32_t lds_addr, uint32_t voffset, uint32_t soffset) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds_addr),
+                 "v"(voffset), "s"(rsrc), "s"(soffset)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ void dma_dword(v4i_rsrc rsrc, uint32_t lds_addr, uint32_t voffset, uint32_t soffset) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds" ::"s"(lds_addr),
+                 "v"(voffset), "s"(rsrc), "s"(soffset)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_address(const void *p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint8_t *)p));
 }
 
 // Buffer resource over [p, p + bytes): loads past the end return zeros, which

@@ -46,37 +46,6 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
 typedef unsigned v2u __attribute__((ext_vector_type(2)));
 
-typedef int v4i_rsrc __attribute__((ext_vector_type(4)));
-
-// Raw buffer resource (base, size in bytes; loads past the end return zero)
-// as four scalar dwords for the inline loads below.
-__device__ __forceinline__ v4i_rsrc raw_rsrc(const void *p, uint32_t bytes) {
-    const uint64_t a = reinterpret_cast<uint64_t>(p);
-    return v4i_rsrc{static_cast<int>(a), static_cast<int>((a >> 32) & 0xFFFF), static_cast<int>(bytes), 0x00020000};
-}
-
-// Direct-to-LDS buffer loads, written as inline asm so the compiler does not
-// track them: it would otherwise make every LDS read and every barrier wait
-// for all of them, including the loads of later groups into other slots.
-// Their completion is counted explicitly with s_waitcnt vmcnt.  Lane i's
-// data lands at lds_addr + 16 i (12-byte form) or + 4 i (4-byte form).
-// Nothing else in these kernels uses M0.
-__device__ __forceinline__ void dma_dwordx3(v4i_rsrc rsrc, uint32_t lds_addr, uint32_t voffset, uint32_t soffset) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx3 %1, %2, %3 offen lds" ::"s"(lds_addr),
-                 "v"(voffset), "s"(rsrc), "s"(soffset)
-                 : "memory", "m0");
-}
-
-__device__ __forceinline__ void dma_dword(v4i_rsrc rsrc, uint32_t lds_addr, uint32_t voffset, uint32_t soffset) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds" ::"s"(lds_addr),
-                 "v"(voffset), "s"(rsrc), "s"(soffset)
-                 : "memory", "m0");
-}
-
-__device__ __forceinline__ uint32_t lds_address(const void *p) {
-    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint8_t *)p));
-}
-
 // f(std::integral_constant<int, I>) for I = 0 .. N-1, in order.
 template <int N, typename F, int... I>
 __device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
