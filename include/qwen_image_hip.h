@@ -133,10 +133,13 @@ int qi_hip_w4a16_gemv(const void *x_half, const void *w_tiled_codes, const void 
 /* fp6 operand path for W4A4.  The int4 codes -7..7 are exact in FP6 E2M3, so
  * the gfx950 f8f6f4 MFMA (32x32x64: K = one g64 group) yields the same exact
  * per-group integer partials as the int8 MFMA, already in fp32.  Layout of
- * both operands: per 32-row tile T and 64-group g, 1536 bytes = 2 halves x
- * 64 lanes x 12 bytes; lane l of half h holds the E2M3 codes (6 bits each,
- * little-endian) of inputs 32*(l/32) + 16h .. + 15 of the group, row
- * 32T + l%32.  Scales [rows/32][G][32] fp16 (tile, group, row).
+ * both operands (7/8 byte per input): per 32-row tile T and 64-group g, 1792
+ * bytes = half 0 (64 lanes x 16 bytes) then half 1 (64 lanes x 12 bytes);
+ * lane l of half h holds the E2M3 codes (6 bits each, little-endian) of
+ * inputs 32*(l/32) + 16h .. + 15 of the group, row 32T + l%32, and bytes
+ * 12..15 of a half-0 slot hold that row's fp16 group scale, zero-extended.
+ * The optional separate scale arrays are [rows/32][G][32] fp16 (tile, group,
+ * row); pass NULL to skip them.
  *
  * Quantiser (same arithmetic and codes as qi_w4a4_quantize_activations):
  * x is f32 (x_is_half = 0) or fp16 [m, k]; codes6 holds ceil(m/32) * 32 rows
@@ -145,16 +148,16 @@ int qi_hip_w4a16_gemv(const void *x_half, const void *w_tiled_codes, const void 
 int qi_hip_w4a4_quantize_activations_fp6(const void *x, int x_is_half, void *codes6, void *scales_tiled, int m,
                                          int k, void *stream);
 /* One-time re-layout of QIPACK W4A4 weights (codes [n, k/2], scales [n, G])
- * into the fp6 operand layout above (3/4 byte per weight) plus tiled scales.
+ * into the fp6 operand layout above, plus (unless NULL) tiled scales.
  * n % 32 == 0, k % 256 == 0. */
 int qi_hip_relayout_w4a4_fp6(const void *codes, const void *scales, void *codes6, void *tiled_scales, int n, int k,
                              void *stream);
-/* W4A4 GEMM on the fp6 operands; same result, bit for bit, as
- * qi_hip_w4a4_gemm_tiled on the same codes.  Any m >= 1; n % 32 == 0;
- * k % 256 == 0; y aligned to 16 bytes (f32) or 8 bytes (f16). */
-int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *a_scales_tiled, const void *w_codes6,
-                         const void *w_scales_tiled, const float *bias, void *y, int out_type, int epilogue, int m,
-                         int n, int k, void *stream);
+/* W4A4 GEMM on the fp6 operands (scales read from the code blocks); same
+ * result, bit for bit, as qi_hip_w4a4_gemm_tiled on the same codes.  Any
+ * m >= 1; n % 32 == 0; k % 256 == 0; both code buffers 16-byte aligned; y
+ * aligned to 16 bytes (f32) or 8 bytes (f16). */
+int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *w_codes6, const float *bias, void *y, int out_type,
+                         int epilogue, int m, int n, int k, void *stream);
 
 /* Device-side QIPACK quantiser (int4_pack.cplus:237-468 arithmetic, bit-exact):
  * w_half fp16 [n, k] -> QIPACK arrays.  scheme 5 = W4A16 affine (minimums

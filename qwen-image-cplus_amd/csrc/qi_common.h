@@ -22,6 +22,10 @@ namespace qi {
 
 constexpr int GROUP = 64;      // QIPACK v6 group size along K
 constexpr int WAVE = 64;       // CDNA wavefront
+// fp6 operand blocks (one 32-row tile, one group): half 0 = 64 lanes x 16
+// bytes (12 code bytes + the row's fp16 scale + 2 zero bytes), then half 1 =
+// 64 lanes x 12 code bytes.
+constexpr unsigned FP6_HALF0 = 1024, FP6_BLOCK = 1792;
 
 inline hipStream_t stream_of(void *s) { return reinterpret_cast<hipStream_t>(s); }
 

@@ -49,10 +49,12 @@ __device__ __forceinline__ void load4<uint16_t>(const uint16_t *src, float v[4])
 }
 
 // FMT 0: QIPACK activation layout (codes [m, k/2] nibbles, scales [m, k/64]).
-// FMT 1: fp6 MFMA-operand layout: per 32-row tile T and group g, 1536 bytes
-//        = 2 halves x 64 lanes x 12 bytes; lane l of half h holds the E2M3
-//        codes (6 bits each, little-endian) of inputs 32 * (l / 32) + 16h ..
-//        + 15 of the group, row 32T + l % 32.  Scales [m/32][G][32] fp16.
+// FMT 1: fp6 MFMA-operand layout: per 32-row tile T and group g, 1792 bytes
+//        = half 0 (64 lanes x 16 bytes) then half 1 (64 lanes x 12 bytes);
+//        lane l of half h holds the E2M3 codes (6 bits each, little-endian)
+//        of inputs 32 * (l / 32) + 16h .. + 15 of the group, row 32T + l % 32;
+//        bytes 12..15 of a half-0 slot hold that row's fp16 scale, zero-
+//        extended.  Scales also [m/32][G][32] fp16.
 // LDS word of element i of a chunk: an XOR swizzle that makes every access
 // pattern below (4 consecutive words per lane, and the strided butterfly
 // quadruples of strides 4, 16, 64) conflict-free for 32 lanes at a time.
@@ -143,21 +145,22 @@ __global__ __launch_bounds__(QUANT_WAVES * WAVE) void quantize_chunks_kernel(
             // This lane's four inputs are 4p..4p+3 of slice sl of group g
             // (inputs 16 sl .. 16 sl + 15).  Slice sl goes to half sl & 1 of
             // the (32-row tile, group) block, lane slot 32 (sl >> 1) + row %
-            // 32, whose 12 bytes are the 24-bit runs of lanes p = 0..3: lane
-            // p < 3 assembles and stores dword p.
+            // 32, whose 12 code bytes are the 24-bit runs of lanes p = 0..3:
+            // lane p < 3 assembles and stores dword p.  In half 0 (16-byte
+            // slots) lane p = 3 stores the scale as dword 3.
             const int sl = (lane & 15) >> 2, p = lane & 3;
             const uint32_t bits =
                 e2m3_of(q[0]) | (e2m3_of(q[1]) << 6) | (e2m3_of(q[2]) << 12) | (e2m3_of(q[3]) << 18);
             const uint32_t next = static_cast<uint32_t>(__shfl_down(static_cast<int>(bits), 1, 64));
             const uint32_t block = (row >> 5) * (k >> 6) + g;
-            const uint32_t r32 = row & 31;
-            if (p < 3) {
-                const uint32_t word = (bits >> (8 * p)) | (next << (24 - 8 * p));
-                uint32_t *dst = reinterpret_cast<uint32_t *>(codes + static_cast<size_t>(block) * 1536 +
-                                                             (sl & 1) * 768 + ((sl >> 1) * 32 + r32) * 12);
-                dst[p] = word;
-            }
-            if ((lane & 15) == 0) scales[static_cast<size_t>(block) * 32 + r32] = scale_bits;
+            const uint32_t r32 = row & 31, slot = (sl >> 1) * 32 + r32;
+            uint32_t *dst = reinterpret_cast<uint32_t *>(codes + static_cast<size_t>(block) * FP6_BLOCK +
+                                                         ((sl & 1) ? FP6_HALF0 + slot * 12 : slot * 16));
+            if (p < 3)
+                dst[p] = (bits >> (8 * p)) | (next << (24 - 8 * p));
+            else if ((sl & 1) == 0)
+                dst[3] = scale_bits;
+            if (scales && (lane & 15) == 0) scales[static_cast<size_t>(block) * 32 + r32] = scale_bits;
         }
     }
 }
@@ -182,7 +185,9 @@ __global__ void f32_to_f16_kernel(const float *__restrict__ src, uint16_t *__res
 
 template <typename In, int FMT>
 static int launch_quantize(const In *x, void *codes, void *scales, int m, int k, hipStream_t stream) {
-    if (m < 0 || k <= 0 || k % 256 != 0 || (m > 0 && (!x || !codes || !scales))) return kInvalid;
+    // The fp6 layout carries the scales inside the code blocks; its separate
+    // scale array is optional (null: not written).
+    if (m < 0 || k <= 0 || k % 256 != 0 || (m > 0 && (!x || !codes || (FMT == 0 && !scales)))) return kInvalid;
     if (m == 0) return 0;
     // Vector loads: 4 elements per lane; 2-byte (QIPACK) or 4-byte (fp6) code stores.
     if (reinterpret_cast<uintptr_t>(x) % (4 * sizeof(In)) != 0 ||

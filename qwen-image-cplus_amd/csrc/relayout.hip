@@ -91,10 +91,13 @@ __global__ void relayout_scales(const uint16_t *__restrict__ scales, const uint1
 }
 
 // W4A4 weights as fp6 MFMA operands, the layout the activation quantiser
-// writes: per 32-row tile T and group g, 2 halves x 64 lanes x 12 bytes; lane
-// l of half h holds the E2M3 codes of inputs 32 * (l / 32) + 16h .. + 15 of
-// row 32T + l % 32.  One thread per 12-byte lane slot.
-__global__ void relayout_w4a4_fp6_codes(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int n, int k) {
+// writes: per 32-row tile T and group g, half 0 (64 lanes x 16 bytes) then
+// half 1 (64 lanes x 12 bytes); lane l of half h holds the E2M3 codes of
+// inputs 32 * (l / 32) + 16h .. + 15 of row 32T + l % 32, and bytes 12..15 of
+// a half-0 slot hold that row's fp16 scale, zero-extended.  One thread per
+// lane slot.
+__global__ void relayout_w4a4_fp6_codes(const uint8_t *__restrict__ src, const uint16_t *__restrict__ scales,
+                                        uint8_t *__restrict__ dst, int n, int k) {
     const int groups = k / GROUP;
     const long long total = static_cast<long long>(n / 32) * groups * 2 * WAVE;
     for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
@@ -117,10 +120,11 @@ __global__ void relayout_w4a4_fp6_codes(const uint8_t *__restrict__ src, uint8_t
             out[bit >> 5] |= v << (bit & 31);
             if ((bit & 31) > 26) out[(bit >> 5) + 1] |= v >> (32 - (bit & 31));
         }
-        uint8_t *d = dst + i * 12;
+        uint8_t *d = dst + tg * FP6_BLOCK + (half ? FP6_HALF0 + lane * 12 : lane * 16);
         *reinterpret_cast<uint32_t *>(d) = out[0];
         *reinterpret_cast<uint32_t *>(d + 4) = out[1];
         *reinterpret_cast<uint32_t *>(d + 8) = out[2];
+        if (!half) *reinterpret_cast<uint32_t *>(d + 12) = scales[row * groups + g];
     }
 }
 
@@ -218,13 +222,14 @@ QI_API int qi_hip_relayout_w4a16_inverse(const void *tiled_codes, const void *ti
 
 QI_API int qi_hip_relayout_w4a4_fp6(const void *codes, const void *scales, void *codes6, void *tiled_scales, int n,
                                     int k, void *stream) {
-    if (n <= 0 || k <= 0 || n % 32 || k % 256 || !codes || !scales || !codes6 || !tiled_scales) return kInvalid;
+    if (n <= 0 || k <= 0 || n % 32 || k % 256 || !codes || !scales || !codes6) return kInvalid;
     if (!aligned(codes, 8) || !aligned(codes6, 4) || !aligned(scales, 2) || !aligned(tiled_scales, 2)) return kInvalid;
     hipStream_t s = stream_of(stream);
     const long long slots = static_cast<long long>(n / 32) * (k / GROUP) * 2 * WAVE;
-    relayout_w4a4_fp6_codes<<<grid_for(slots, 256), 256, 0, s>>>(static_cast<const uint8_t *>(codes),
-                                                                  static_cast<uint8_t *>(codes6), n, k);
-    relayout_fp6_weight_scales<<<grid_for(static_cast<long long>(n) * (k / GROUP), 256), 256, 0, s>>>(
+    relayout_w4a4_fp6_codes<<<grid_for(slots, 256), 256, 0, s>>>(
+        static_cast<const uint8_t *>(codes), static_cast<const uint16_t *>(scales), static_cast<uint8_t *>(codes6), n, k);
+    if (tiled_scales)  // optional: the GEMM reads the scales from codes6
+        relayout_fp6_weight_scales<<<grid_for(static_cast<long long>(n) * (k / GROUP), 256), 256, 0, s>>>(
         static_cast<const uint16_t *>(scales), static_cast<uint16_t *>(tiled_scales), n, k);
     return launch_status();
 }

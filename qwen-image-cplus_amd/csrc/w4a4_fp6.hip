@@ -15,23 +15,23 @@
 // Results are bit-identical to the reference formula.
 //
 // Layouts (written by qi_hip_w4a4_quantize_activations_fp6 and
-// qi_hip_relayout_w4a4_fp6): per 32-row tile T and group g, 1536 bytes = two
-// halves of 64 lanes x 12 bytes; lane l of half h holds the E2M3 codes of
-// inputs 32 * (l / 32) + 16h .. + 15 of row 32T + l % 32, which is the lane's
-// MFMA operand (6 dwords) split in two.  Scales [rows/32][G][32] fp16 for
-// both operands.
+// qi_hip_relayout_w4a4_fp6): per 32-row tile T and group g, 1792 bytes = half
+// 0 (64 lanes x 16 bytes) then half 1 (64 lanes x 12 bytes); lane l of half h
+// holds the E2M3 codes of inputs 32 * (l / 32) + 16h .. + 15 of row
+// 32T + l % 32, which is the lane's MFMA operand (6 dwords) split in two.
+// Bytes 12..13 of a half-0 lane slot hold the fp16 group scale of row
+// 32T + l % 32 (bytes 14..15 are zero), so the scales arrive with the codes.
 //
 // Roles.  The MFMA A operand is the weight tile (32 outputs n), B the
 // activation tile (32 rows m).  Lane l's accumulator register 4a + r then
 // holds y[m = l % 32][n = 8a + 4 * (l / 32) + r]: four consecutive outputs,
 // stored with one wide write.
 //
-// Pipeline.  A ring of NSTAGE LDS slots holds the operand and scale blocks
-// of upcoming groups, filled NSTAGE-1 groups ahead by buffer_load ... lds
-// (12 bytes per lane for operands: one instruction per 768-byte half block,
-// landing at a 16-byte lane pitch; 4 bytes per lane for scales).  One barrier
-// per group; each group's matrix-core work is issued before the barrier and
-// the next group's LDS reads overlap its fp32 step.
+// Pipeline.  A ring of NSTAGE LDS slots holds the operand blocks of
+// upcoming groups, filled NSTAGE groups ahead by buffer_load ... lds (16
+// bytes per lane, landing at a 16-byte lane pitch).  One barrier per group.
+// The matrix-core work of group g + 1 is interleaved, tile by tile, with the
+// fp32 step of group g, so the two units work side by side within a wave.
 
 #include <cstdlib>
 #include <utility>
@@ -65,8 +65,7 @@ __device__ __forceinline__ v8i fp6_operand(v4i lo, v4i hi) {
 
 template <int TM, int TN, int WM, int WN, int NSTAGE>
 __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2))) void w4a4_fp6_kernel(
-    const uint8_t *__restrict__ a6, const uint16_t *__restrict__ sa_t, const uint8_t *__restrict__ w6,
-    const uint16_t *__restrict__ sw_t, const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi,
+    const uint8_t *__restrict__ a6, const uint8_t *__restrict__ w6, const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi,
     int m, int n, int k) {
     constexpr int NW = WM * WN;
     constexpr int MT = WM * TM, NTL = WN * TN;  // 32-row tiles of the block
@@ -74,13 +73,12 @@ __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2)
     constexpr int HALVES = 2 * (MT + NTL);      // 768-byte loads per group
     static_assert(HALVES % NW == 0, "loader mapping");
     constexpr int L_PER_W = HALVES / NW;
-    static_assert(TM <= 4 && TN <= 2, "one scale load per operand per wave; scale products pair the n-tiles");
-    constexpr int LOADS_PER_GROUP = L_PER_W + 2;  // per wave: operands + sa + sw
+    static_assert(TN <= 2, "scale products pair the n-tiles");
+    constexpr int LOADS_PER_GROUP = L_PER_W;  // per wave
     constexpr int TILE = 2048, SLOT = (MT + NTL) * TILE;
-    constexpr int SC_WAVE = 512, SC_SLOT = NW * SC_WAVE;  // scale bytes per wave / per slot
-    static_assert(NSTAGE * (SLOT + SC_SLOT) <= 160 * 1024, "LDS size");
+    constexpr uint32_t BLOCK = FP6_BLOCK;  // global bytes per (tile, group)
+    static_assert(NSTAGE * SLOT <= 160 * 1024, "LDS size");
     __shared__ __attribute__((aligned(16))) uint8_t lds[NSTAGE * SLOT];
-    __shared__ __attribute__((aligned(16))) uint8_t lds_sc[NSTAGE * SC_SLOT];
 
     const int groups = k >> 6;
     const int lane = threadIdx.x & (WAVE - 1);
@@ -93,12 +91,10 @@ __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2)
     const int mt0 = tm * MT, nt0 = tn * NTL;  // first 32-row tiles
     const int m_tiles = (m + 31) / 32, n_tiles = n / 32;
 
-    const uint32_t a_bytes = static_cast<uint32_t>(m_tiles) * groups * 1536u;
-    const uint32_t w_bytes = static_cast<uint32_t>(n_tiles) * groups * 1536u;
+    const uint32_t a_bytes = static_cast<uint32_t>(m_tiles) * groups * BLOCK;
+    const uint32_t w_bytes = static_cast<uint32_t>(n_tiles) * groups * BLOCK;
     const v4i_rsrc ra = raw_rsrc(a6, a_bytes);
     const v4i_rsrc rw = raw_rsrc(w6, w_bytes);
-    const v4i_rsrc rsa = raw_rsrc(sa_t, static_cast<uint32_t>(m_tiles) * groups * 64u);
-    const v4i_rsrc rsw = raw_rsrc(sw_t, static_cast<uint32_t>(n_tiles) * groups * 64u);
 
     // This wave's operand loads: half blocks H0 .. H0 + L_PER_W - 1 of the
     // block's (MT + NTL) tiles, activation tiles first.  Missing tiles read
@@ -111,31 +107,23 @@ __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2)
         const bool from_a = H < 2 * MT;
         const int t = from_a ? mt0 + X : nt0 + X - MT;
         const bool ok = from_a ? t < m_tiles : t < n_tiles;
-        vo[u] = ok ? static_cast<uint32_t>(t) * groups * 1536u + half * 768u + lane * 12u
+        vo[u] = ok ? static_cast<uint32_t>(t) * groups * BLOCK + (half ? 1024u + lane * 12u : lane * 16u)
                    : (from_a ? a_bytes : w_bytes);
     }
-    // Scales, also loaded straight into LDS (so that every vector-memory load
-    // of the loop is a direct-to-LDS load whose completion this code counts
-    // itself): per wave and group, one 4-byte-per-lane load gathers the 64
-    // bytes of each of its TM activation tiles (lanes 16i .. 16i+15) and one
-    // those of its TN weight tiles.  Lanes past TM / TN read zeros.
-    uint32_t sa_vo, sw_vo;
-    {
-        const int i = lane >> 4, t = mt0 + wm * TM + i;
-        sa_vo = i < TM && t < m_tiles ? static_cast<uint32_t>(t) * groups * 64u + (lane & 15) * 4u : 0x7FFFFFF0u;
-        const int tw = nt0 + wn * TN + i;
-        sw_vo = i < TN && tw < n_tiles ? static_cast<uint32_t>(tw) * groups * 64u + (lane & 15) * 4u : 0x7FFFFFF0u;
-    }
 
-    const uint32_t lds0 = lds_address(lds), sc0 = lds_address(lds_sc);
+    // Every vector-memory load of the loop is a direct-to-LDS load whose
+    // completion this code counts itself, and every one moves 16 bytes per
+    // lane.  In half 1 (12-byte lane stride) a lane's last 4 bytes are the
+    // next lane's codes, or bytes past the buffer, which read as zero; they
+    // land in the slot's unused fourth dword.
+    const uint32_t lds0 = lds_address(lds);
     auto issue = [&](int g, int slot) {
 #pragma unroll
         for (int u = 0; u < L_PER_W; ++u) {
             const int H = H0 + u;
-            dma_dwordx3(H < 2 * MT ? ra : rw, lds0 + slot * SLOT + (H >> 1) * TILE + (H & 1) * 1024, vo[u], g * 1536);
+            dma_dwordx4(H < 2 * MT ? ra : rw, lds0 + slot * SLOT + (H >> 1) * TILE + (H & 1) * 1024, vo[u],
+                        g * BLOCK);
         }
-        dma_dword(rsa, sc0 + slot * SC_SLOT + wave * SC_WAVE, sa_vo, g * 64);
-        dma_dword(rsw, sc0 + slot * SC_SLOT + wave * SC_WAVE + 256, sw_vo, g * 64);
     };
 
     v16f acc[TN][TM];
@@ -148,13 +136,11 @@ __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2)
 
     // This lane's fragments: weight tile j half h at
     // lds[slot][MT + wn * TN + j][h][16 lane], activation tile i likewise.
-    // Scales inside the wave's scale block: sa of row l % 32 of tile i at
-    // 64i + 2 (l % 32); the weight scale at 256 + 64 (l / 32) + 2 (l % 32),
-    // i.e. output l % 32 of n-tile l / 32.
+    // The fourth dword of a half-0 slot is the scale of row l % 32: sa of
+    // activation tile i, and for the weight, output l % 32 of n-tile l / 32
+    // (the outer product's block l / 32).
     const uint8_t *w_frag = lds + (MT + wn * TN) * TILE + lane * 16;
     const uint8_t *x_frag = lds + wm * TM * TILE + lane * 16;
-    const uint8_t *sa_lds = lds_sc + wave * SC_WAVE + r32 * 2;
-    const uint8_t *sw_lds = lds_sc + wave * SC_WAVE + 256 + lane * 2;
 
     struct Frags {  // raw LDS reads; converted where consumed
         v8i wf[TN], xf[TM];
@@ -162,75 +148,80 @@ __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2)
     };
     auto read_frags = [&](auto slot_c, Frags &F) {
         constexpr int slot = decltype(slot_c)::value;
+        uint32_t sw[TN];
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             const v4i lo = *reinterpret_cast<const v4i *>(w_frag + slot * SLOT + j * TILE);
             const v4i hi = *reinterpret_cast<const v4i *>(w_frag + slot * SLOT + j * TILE + 1024);
             F.wf[j] = fp6_operand(lo, hi);
+            sw[j] = static_cast<uint32_t>(lo[3]);
         }
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             const v4i lo = *reinterpret_cast<const v4i *>(x_frag + slot * SLOT + i * TILE);
             const v4i hi = *reinterpret_cast<const v4i *>(x_frag + slot * SLOT + i * TILE + 1024);
             F.xf[i] = fp6_operand(lo, hi);
-            F.sal[i] = *reinterpret_cast<const uint16_t *>(sa_lds + slot * SC_SLOT + 64 * i);
+            F.sal[i] = static_cast<uint32_t>(lo[3]);
         }
-        F.swl = *reinterpret_cast<const uint16_t *>(sw_lds + slot * SC_SLOT);
+        // Lanes 32..63 supply block 1 of the outer product (n-tile 1); with
+        // one n-tile that block is unused.
+        F.swl = TN == 1 ? sw[0] : (lane < 32 ? sw[0] : sw[TN - 1]);
     };
-    // Matrix-core work of one group: the scale outer products and the
-    // partial tiles.  Block b of the 32x32x1 outer product has rows = outputs
-    // of n-tile b (lanes 32b .. 32b+31 supply them) and columns = rows m of
-    // tile i; its result registers 16b .. 16b+15 line up with the
-    // accumulator registers.
+    // Matrix-core work: the scale outer products and the partial tiles.
+    // Block b of the 32x32x1 outer product has rows = outputs of n-tile b
+    // (lanes 32b .. 32b+31 supply them) and columns = rows m of tile i; its
+    // result registers 16b .. 16b+15 line up with the accumulator registers.
     v32f sp[TM];
     v16f p[TN][TM];
-    auto mfma = [&](const Frags &F) {
+    auto scale_mfma = [&](const Frags &F, int i) {
+        v32f z32;
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            v32f z32;
-#pragma unroll
-            for (int r = 0; r < 32; ++r) z32[r] = 0.f;
-            sp[i] = __builtin_amdgcn_mfma_f32_32x32x1f32(h2f(static_cast<uint16_t>(F.swl)),
-                                                         h2f(static_cast<uint16_t>(F.sal[i])), z32, 0, 0, 0);
-        }
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int i = 0; i < TM; ++i) {
-                v16f z;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) z[r] = 0.f;
-                // fmt 2 = FP6 E2M3 for both operands; block scales 2^0.
-                p[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(F.wf[j], F.xf[i], z, 2, 2, 0, 127, 0, 127);
-            }
+        for (int r = 0; r < 32; ++r) z32[r] = 0.f;
+        sp[i] = __builtin_amdgcn_mfma_f32_32x32x1f32(h2f(static_cast<uint16_t>(F.swl)),
+                                                     h2f(static_cast<uint16_t>(F.sal[i])), z32, 0, 0, 0);
     };
-    // The exact fp32 step of one group, in ascending group order.
-    auto fmas = [&]() {
+    auto tile_mfma = [&](const Frags &F, int j, int i) {
+        v16f z;
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+        for (int r = 0; r < 16; ++r) z[r] = 0.f;
+        // fmt 2 = FP6 E2M3 for both operands; block scales 2^0.
+        p[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(F.wf[j], F.xf[i], z, 2, 2, 0, 127, 0, 127);
+    };
+    // The exact fp32 step of one tile and group, in ascending group order.
+    auto tile_fma = [&](int j, int i) {
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[j][i][r] = __builtin_fmaf(p[j][i][r], sp[i][16 * j + r], acc[j][i][r]);
+        for (int r = 0; r < 16; ++r) acc[j][i][r] = __builtin_fmaf(p[j][i][r], sp[i][16 * j + r], acc[j][i][r]);
     };
 
-    // Software pipeline, per group g (slots are g mod NSTAGE):
-    //   matrix-core work of g (fragments read during g - 1);
+    // Software pipeline.  The matrix-core work of group g + 1 runs during
+    // the fp32 step of group g, interleaved tile by tile: the fp32 step of
+    // tile (j, i) frees p[j][i], whose next partial tile is issued at once and
+    // computes while the vector unit steps the next tile; sp[i] is refilled
+    // once both n-tiles of row tile i have used it.  So the fragments are
+    // needed one group ahead only.  Per group g (slots are g mod NSTAGE):
     //   wait until this wave's loads of g + 1 are done, barrier (then every
-    //   wave's are, and every wave has consumed its reads of slot g - 1);
-    //   issue the loads of g + NSTAGE - 1 into slot g - 1;
-    //   read the fragments of g + 1, which land during
-    //   the fp32 step of g.
+    //   wave's are, and every wave has consumed its reads of slot g);
+    //   issue the loads of g + NSTAGE into slot g;
+    //   read the fragments of g + 1;
+    //   fp32 step of g interleaved with the matrix-core work of g + 1.
     // Loads past the last group read harmless bytes into slots that are
-    // never consumed and keep the loads per group constant.
+    // never consumed, keeping the loads per group constant; the last step's
+    // matrix-core work is likewise discarded.
     static_assert(NSTAGE % 4 == 0, "whole quarters of the ring per group count (groups % 4 == 0)");
-    Frags F[2];
+    static_assert(NSTAGE >= 2 && (NSTAGE - 1) * LOADS_PER_GROUP <= 63, "vmcnt range");
+    Frags F;
 #pragma unroll
-    for (int q = 0; q < NSTAGE - 1; ++q) issue(q, q);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTAGE - 2) * LOADS_PER_GROUP) : "memory");
+    for (int q = 0; q < NSTAGE; ++q) issue(q, q);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTAGE - 1) * LOADS_PER_GROUP) : "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    read_frags(std::integral_constant<int, 0>{}, F[0]);
+    read_frags(std::integral_constant<int, 0>{}, F);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        scale_mfma(F, i);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) tile_mfma(F, j, i);
+    }
     for (int g0 = 0; g0 < groups; g0 += NSTAGE) {
         static_for<NSTAGE>([&](auto uc) {
             constexpr int u = decltype(uc)::value;
@@ -238,25 +229,42 @@ __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2)
             // groups is a multiple of 4, so only whole quarters of a
             // NSTAGE = 8 ring can be missing at the end; the test is uniform
             // and covers a whole iteration, so no partial tile stays live
-            // across iterations.  After the last group the reads of group
-            // `groups` fetch harmless slot contents that are never used.
+            // across iterations.
             if (u < 4 || g < groups) {
-                // Scheduling fences pin the phase order: the compiler would
-                // otherwise sink the matrix-core work below the barrier and
-                // the next group's reads, and wait for those reads.
+                // Scheduling fences pin the order; without them the compiler
+                // gathers the matrix-core work into one block.  A bare
+                // s_barrier: __syncthreads' release fence would also wait for
+                // the loads of the groups still in flight.
                 __builtin_amdgcn_sched_barrier(0);
-                mfma(F[u & 1]);
-                __builtin_amdgcn_sched_barrier(0);
-                // A bare s_barrier: __syncthreads' release fence would also
-                // wait for the loads of the groups still in flight.
-                asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((NSTAGE - 3) * LOADS_PER_GROUP) : "memory");
+                asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((NSTAGE - 2) * LOADS_PER_GROUP) : "memory");
                 __builtin_amdgcn_s_barrier();
                 asm volatile("" ::: "memory");
-                issue(g + NSTAGE - 1, (u + NSTAGE - 1) % NSTAGE);
-                read_frags(std::integral_constant<int, (u + 1) % NSTAGE>{}, F[(u + 1) & 1]);
+                issue(g + NSTAGE, u);
+                read_frags(std::integral_constant<int, (u + 1) % NSTAGE>{}, F);
                 __builtin_amdgcn_sched_barrier(0);
-                fmas();
-                __builtin_amdgcn_sched_barrier(0);
+                // Tile q = i * TN + j.  Its next partial tile is issued LAG
+                // tiles later, so the fragment reads above have the fp32
+                // steps of LAG tiles to land.
+                constexpr int T = TM * TN, LAG = T > 2 ? 2 : 0;
+                static_for<T + LAG>([&](auto qc) {
+                    constexpr int q = decltype(qc)::value;
+                    if constexpr (q < T) {
+                        constexpr int i = q / TN, j = q % TN;
+                        tile_fma(j, i);
+                        __builtin_amdgcn_sched_barrier(0);
+                        // sp[i] is free once the last tile of row tile i has
+                        // stepped.
+                        if constexpr (j == TN - 1) {
+                            scale_mfma(F, i);
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                    }
+                    if constexpr (q >= LAG) {
+                        constexpr int d = q - LAG;
+                        tile_mfma(F, d % TN, d / TN);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                });
             }
         });
     }
@@ -293,14 +301,13 @@ __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2)
 }
 
 template <int TM, int TN, int WM, int WN, int NSTAGE>
-static int launch_fp6(const void *a6, const void *sa, const void *w6, const void *sw, const float *bias, void *y,
+static int launch_fp6(const void *a6, const void *w6, const float *bias, void *y,
                       int out_type, int epi, int m, int n, int k, hipStream_t stream) {
     constexpr int BM = WM * TM * 32, BN = WN * TN * 32;
     const long long blocks = static_cast<long long>((m + BM - 1) / BM) * ((n + BN - 1) / BN);
     if (blocks > 0x7FFFFFFFLL) return kInvalid;
     w4a4_fp6_kernel<TM, TN, WM, WN, NSTAGE><<<dim3(static_cast<unsigned>(blocks)), dim3(WM * WN * WAVE), 0, stream>>>(
-        static_cast<const uint8_t *>(a6), static_cast<const uint16_t *>(sa), static_cast<const uint8_t *>(w6),
-        static_cast<const uint16_t *>(sw), bias, y, out_type, epi, m, n, k);
+        static_cast<const uint8_t *>(a6), static_cast<const uint8_t *>(w6), bias, y, out_type, epi, m, n, k);
     return launch_status();
 }
 
@@ -308,20 +315,18 @@ static int launch_fp6(const void *a6, const void *sa, const void *w6, const void
 
 using namespace qi;
 
-QI_API int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *a_scales_tiled, const void *w_codes6,
-                                const void *w_scales_tiled, const float *bias, void *y, int out_type, int epilogue,
-                                int m, int n, int k, void *stream) {
+QI_API int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *w_codes6, const float *bias, void *y,
+                                int out_type, int epilogue, int m, int n, int k, void *stream) {
     if (m <= 0 || n <= 0 || k <= 0 || n % 32 || k % 256) return kInvalid;
-    if (!a_codes6 || !a_scales_tiled || !w_codes6 || !w_scales_tiled || !y) return kInvalid;
+    if (!a_codes6 || !w_codes6 || !y) return kInvalid;
     if (out_type != QI_HIP_OUT_F32 && out_type != QI_HIP_OUT_F16) return kInvalid;
     if (epilogue != QI_HIP_EPILOGUE_NONE && epilogue != QI_HIP_EPILOGUE_GELU_TANH) return kInvalid;
-    if (reinterpret_cast<uintptr_t>(a_codes6) % 4 || reinterpret_cast<uintptr_t>(w_codes6) % 4 ||
-        reinterpret_cast<uintptr_t>(a_scales_tiled) % 2 || reinterpret_cast<uintptr_t>(w_scales_tiled) % 2 ||
+    if (reinterpret_cast<uintptr_t>(a_codes6) % 16 || reinterpret_cast<uintptr_t>(w_codes6) % 16 ||
         reinterpret_cast<uintptr_t>(y) % (out_type == QI_HIP_OUT_F16 ? 8 : 16))
         return kInvalid;
     const long long g = k / 64;
-    if (static_cast<long long>((m + 31) / 32) * g * 1536 >= (1LL << 31) ||
-        static_cast<long long>(n / 32) * g * 1536 >= (1LL << 31))
+    if (static_cast<long long>((m + 31) / 32) * g * FP6_BLOCK >= (1LL << 31) ||
+        static_cast<long long>(n / 32) * g * FP6_BLOCK >= (1LL << 31))
         return kInvalid;
     hipStream_t s = stream_of(stream);
     // Tile shapes (measured on MI355X): 128 x 128 with four waves when that
@@ -341,22 +346,16 @@ QI_API int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *a_scales_tiled
     if (forced >= 0) cfg = forced;
     switch (cfg) {
     case 0:
-        return launch_fp6<2, 2, 2, 2, 4>(a_codes6, a_scales_tiled, w_codes6, w_scales_tiled, bias, y, out_type,
-                                         epilogue, m, n, k, s);
+        return launch_fp6<2, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, s);
     case 1:
-        return launch_fp6<1, 2, 1, 1, 8>(a_codes6, a_scales_tiled, w_codes6, w_scales_tiled, bias, y, out_type,
-                                         epilogue, m, n, k, s);
+        return launch_fp6<1, 2, 1, 1, 8>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, s);
     case 2:
-        return launch_fp6<2, 2, 1, 1, 8>(a_codes6, a_scales_tiled, w_codes6, w_scales_tiled, bias, y, out_type,
-                                         epilogue, m, n, k, s);
+        return launch_fp6<2, 2, 1, 1, 8>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, s);
     case 3:
-        return launch_fp6<1, 2, 2, 2, 4>(a_codes6, a_scales_tiled, w_codes6, w_scales_tiled, bias, y, out_type,
-                                         epilogue, m, n, k, s);
+        return launch_fp6<1, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, s);
     case 4:
-        return launch_fp6<1, 1, 1, 1, 8>(a_codes6, a_scales_tiled, w_codes6, w_scales_tiled, bias, y, out_type,
-                                         epilogue, m, n, k, s);
+        return launch_fp6<1, 1, 1, 1, 8>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, s);
     default:
-        return launch_fp6<2, 2, 2, 2, 4>(a_codes6, a_scales_tiled, w_codes6, w_scales_tiled, bias, y, out_type,
-                                         epilogue, m, n, k, s);
+        return launch_fp6<2, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, s);
     }
 }

@@ -35,7 +35,7 @@ SIGNATURES: dict[str, list] = {
     "qi_hip_pack_weights": [_p, _p, _p, _p, _i, _i, _i, _i, _p],
     "qi_hip_w4a4_quantize_activations_fp6": [_p, _i, _p, _p, _i, _i, _p],
     "qi_hip_relayout_w4a4_fp6": [_p, _p, _p, _p, _i, _i, _p],
-    "qi_hip_w4a4_gemm_fp6": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
+    "qi_hip_w4a4_gemm_fp6": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
 }
 
 ABI_VERSION = 1

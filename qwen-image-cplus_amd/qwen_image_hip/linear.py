@@ -48,7 +48,7 @@ class PackedLinear:
     n: int
     k: int
     tiled_codes: torch.Tensor
-    tiled_scales: torch.Tensor
+    tiled_scales: torch.Tensor | None  # None for fp6 operands (scales inside the code blocks)
     bias: torch.Tensor | None = None  # fp32 [n] or None (the reference has none)
     operand: str = W4A4_FP6  # W4A4 records only
 
@@ -87,11 +87,12 @@ class Work:
     def __init__(self, rows_max: int, k_max: int, device: torch.device | str = "cuda"):
         self.rows_max = rows_max
         self.k_max = k_max
-        # Sized for the fp6 operand tiles (whole 16-row tiles, 3/4 byte per
-        # input), which also hold the nibble layout (1/2 byte per input).
-        rows16 = ops.fp6_rows(rows_max)
-        self.codes = torch.empty(rows16 * k_max * 3 // 4, dtype=torch.uint8, device=device)
-        self.code_scales = torch.empty(rows16 * k_max // ops.GROUP, dtype=torch.float16, device=device)
+        # Sized for the fp6 operand blocks (whole 32-row tiles, 7/8 byte per
+        # input, scales included), which also hold the nibble layout (1/2
+        # byte per input).
+        rows32 = ops.fp6_rows(rows_max)
+        self.codes = torch.empty(rows32 * ops.fp6_row_bytes(k_max), dtype=torch.uint8, device=device)
+        self.code_scales = torch.empty(rows_max * k_max // ops.GROUP, dtype=torch.float16, device=device)
         self.halves = torch.empty(rows_max * k_max, dtype=torch.float16, device=device)
 
     def views(self, rows: int, k: int):
@@ -104,9 +105,8 @@ class Work:
     def fp6_views(self, rows: int, k: int):
         if rows > self.rows_max or k > self.k_max:
             raise ValueError("work buffers are smaller than this linear")
-        r16 = ops.fp6_rows(rows)
-        return (self.codes[: r16 * k * 3 // 4].view(r16, k * 3 // 4),
-                self.code_scales[: r16 * k // ops.GROUP].view(r16, k // ops.GROUP))
+        r32 = ops.fp6_rows(rows)
+        return self.codes[: r32 * ops.fp6_row_bytes(k)].view(r32, ops.fp6_row_bytes(k))
 
 
 def linear(record: PackedLinear, work: Work, input: torch.Tensor, output: torch.Tensor | None = None,
@@ -124,11 +124,10 @@ def linear(record: PackedLinear, work: Work, input: torch.Tensor, output: torch.
         raise ValueError(f"input width {input.shape[-1]} != record inputs {k}")
     codes, code_scales, halves = work.views(rows, k)
     if record.scheme == SCHEME_W4A4_H256 and record.operand == W4A4_FP6:
-        codes6, scales6 = work.fp6_views(rows, k)
+        codes6 = work.fp6_views(rows, k)
         if not reuse_input:
-            ops.quantize_activations_fp6(input[:rows], codes6, scales6)
-        return ops.w4a4_gemm_fp6(codes6, scales6, record.tiled_codes, record.tiled_scales, rows, record.bias,
-                                 out_dtype, gelu, output)
+            ops.quantize_activations_fp6(input[:rows], codes6)
+        return ops.w4a4_gemm_fp6(codes6, record.tiled_codes, rows, record.bias, out_dtype, gelu, output)
     if record.scheme == SCHEME_W4A4_H256:
         if not reuse_input:
             ops.quantize_activations(input[:rows], codes, code_scales)

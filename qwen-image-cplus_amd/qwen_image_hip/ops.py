@@ -197,17 +197,25 @@ def fp6_rows(m: int) -> int:
     return (m + 31) // 32 * 32
 
 
+def fp6_row_bytes(k: int) -> int:
+    """Bytes of one row of an fp6 operand buffer: 1792 per 32 rows and group."""
+    return k // GROUP * 56
+
+
 def quantize_activations_fp6(x: torch.Tensor, codes6: torch.Tensor | None = None,
-                             scales: torch.Tensor | None = None):
+                             scales: torch.Tensor | None = None, want_scales: bool = False):
     """Quantise rows of x into the fp6 MFMA-operand layout.
 
-    Returns (codes6 uint8 [ceil(m/32)*32, 3k/4], scales fp16 [ceil(m/32)*32, k/64]) in
-    tile order (see qwen_image_hip.h).  Same codes as quantize_activations.
+    Returns (codes6 uint8 [ceil(m/32)*32, 7k/8], scales) in tile order (see
+    qwen_image_hip.h); the code blocks carry the scales.  ``scales`` (fp16
+    [ceil(m/32)*32, k/64], tile order) is also written when given or when
+    ``want_scales``, else None.  Same codes as quantize_activations.
     """
     m, k = x.shape
     rows = fp6_rows(m)
-    codes6 = codes6 if codes6 is not None else _empty((rows, k * 3 // 4), torch.uint8, x)
-    scales = scales if scales is not None else _empty((rows, k // GROUP), torch.float16, x)
+    codes6 = codes6 if codes6 is not None else _empty((rows, fp6_row_bytes(k)), torch.uint8, x)
+    if scales is None and want_scales:
+        scales = _empty((rows, k // GROUP), torch.float16, x)
     if x.dtype not in (torch.float32, torch.float16):
         raise TypeError("activations must be float32 or float16")
     st = load().qi_hip_w4a4_quantize_activations_fp6(_ptr(x), 1 if x.dtype == torch.float16 else 0, _ptr(codes6),
@@ -216,23 +224,22 @@ def quantize_activations_fp6(x: torch.Tensor, codes6: torch.Tensor | None = None
     return codes6, scales
 
 
-def relayout_w4a4_fp6(codes: torch.Tensor, scales: torch.Tensor):
+def relayout_w4a4_fp6(codes: torch.Tensor, scales: torch.Tensor, want_scales: bool = False):
+    """QIPACK W4A4 arrays -> (fp6 operand blocks [n, 7k/8], tiled scales or None)."""
     n, half_k = codes.shape
     k = half_k * 2
-    c6 = _empty((n, k * 3 // 4), torch.uint8, codes)
-    ts = torch.empty_like(scales)
+    c6 = _empty((n, fp6_row_bytes(k)), torch.uint8, codes)
+    ts = torch.empty_like(scales) if want_scales else None
     check(load().qi_hip_relayout_w4a4_fp6(_ptr(codes), _ptr(scales), _ptr(c6), _ptr(ts), n, k, _stream()),
           "relayout")
     return c6, ts
 
 
-def w4a4_gemm_fp6(a_codes6, a_scales_tiled, w_codes6, w_scales_tiled, m: int, bias=None,
-                  out_dtype=torch.float32, gelu=False, y=None):
-    n, k = w_codes6.shape[0], w_codes6.shape[1] * 4 // 3
+def w4a4_gemm_fp6(a_codes6, w_codes6, m: int, bias=None, out_dtype=torch.float32, gelu=False, y=None):
+    n, k = w_codes6.shape[0], w_codes6.shape[1] // 56 * GROUP
     out_type = OUT_F16 if out_dtype == torch.float16 else OUT_F32
     y = y if y is not None else _empty((m, n), out_dtype, w_codes6)
-    st = load().qi_hip_w4a4_gemm_fp6(_ptr(a_codes6), _ptr(a_scales_tiled), _ptr(w_codes6), _ptr(w_scales_tiled),
-                                     _ptr(bias), _ptr(y), out_type, EPILOGUE_GELU_TANH if gelu else EPILOGUE_NONE,
-                                     m, n, k, _stream())
+    st = load().qi_hip_w4a4_gemm_fp6(_ptr(a_codes6), _ptr(w_codes6), _ptr(bias), _ptr(y), out_type,
+                                     EPILOGUE_GELU_TANH if gelu else EPILOGUE_NONE, m, n, k, _stream())
     check(st, "w4a4 gemm")
     return y

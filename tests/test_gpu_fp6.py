@@ -25,13 +25,49 @@ def _u16(t):
     return t.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
 
 
+def fp6_blocks(buf: np.ndarray, rows: int, k: int):
+    """fp6 operand blocks [rows/32][G][1792 B] -> (code bytes [rows/32, G, 2, 64, 12],
+    half-0 slot tails [rows/32, G, 64, 4]).
+
+    Per block: half 0 = 64 lanes x 16 B (12 code bytes, then the row's fp16
+    scale and two zero bytes), half 1 = 64 lanes x 12 code bytes.
+    """
+    G = k // 64
+    blk = buf.reshape(rows // 32, G, 1792)
+    h0 = blk[..., :1024].reshape(rows // 32, G, 64, 16)
+    h1 = blk[..., 1024:].reshape(rows // 32, G, 64, 12)
+    return np.stack([h0[..., :12], h1], axis=2), h0[..., 12:]
+
+
+def fp6_scales(buf: np.ndarray, rows: int, k: int) -> np.ndarray:
+    """The scales carried by fp6 blocks, as [rows, G] fp16 bits (lanes 0..31
+    and 32..63 must agree; the two pad bytes must be zero)."""
+    _, tail = fp6_blocks(buf, rows, k)
+    t = np.ascontiguousarray(tail).view(np.uint16)          # [T, G, 64, 2]
+    assert (t[..., 1] == 0).all()
+    np.testing.assert_array_equal(t[:, :, :32, 0], t[:, :, 32:, 0])
+    return t[:, :, :32, 0].transpose(0, 2, 1).reshape(rows, k // 64)
+
+
+def set_fp6_scales(buf: np.ndarray, rows: int, k: int, scales: np.ndarray) -> np.ndarray:
+    """Copy of fp6 blocks with the carried scales replaced by [rows, G] fp16 bits."""
+    G = k // 64
+    out = buf.copy().reshape(rows // 32, G, 1792)
+    h0 = out[..., :1024].reshape(rows // 32, G, 64, 16)
+    s = np.ascontiguousarray(scales.reshape(rows // 32, 32, G).transpose(0, 2, 1)).astype(np.uint16)
+    for half in range(2):
+        h0[:, :, 32 * half:32 * half + 32, 12:14] = s.view(np.uint8).reshape(rows // 32, G, 32, 2)
+    out[..., :1024] = h0.reshape(rows // 32, G, 1024)
+    return out.reshape(buf.shape)
+
+
 def decode_fp6_tiles(buf: np.ndarray, rows: int, k: int) -> np.ndarray:
-    """fp6 operand tiles [rows/32][G][2 halves][64 lanes][12 B] -> int codes [rows, k].
+    """fp6 operand blocks -> int codes [rows, k].
 
     Lane l of half h holds inputs 32 * (l // 32) + 16h .. + 15 of row l % 32.
     """
     G = k // 64
-    b = buf.reshape(rows // 32, G, 2, 64, 12).astype(np.uint32)
+    b = fp6_blocks(buf, rows, k)[0].astype(np.uint32)
     b = np.concatenate([b, np.zeros(b.shape[:-1] + (1,), np.uint32)], axis=-1)
     vals = np.zeros(b.shape[:-1] + (16,), np.int64)
     lut = np.zeros(64, np.int64)
@@ -65,10 +101,12 @@ def test_fp6_quantizer_matches_codes(dev, m, k, half):
     x = heavy_tailed(m, k, 31 + m)
     xin = x.astype(np.float16) if half else x
     want_c, want_s = oracle.quantize_activations(xin.view(np.uint16) if half else xin)
-    c6, s6 = ops.quantize_activations_fp6(_dev(xin, dev))
+    c6, s6 = ops.quantize_activations_fp6(_dev(xin, dev), want_scales=True)
     rows = ops.fp6_rows(m)
-    codes = decode_fp6_tiles(c6.cpu().numpy(), rows, k)[:m]
+    buf = c6.cpu().numpy()
+    codes = decode_fp6_tiles(buf, rows, k)[:m]
     np.testing.assert_array_equal(codes, unpack_nibbles(want_c))
+    np.testing.assert_array_equal(fp6_scales(buf, rows, k)[:m], want_s)
     got_s = _u16(s6).reshape(rows // 32, k // 64, 32).transpose(0, 2, 1).reshape(rows, k // 64)
     np.testing.assert_array_equal(got_s[:m], want_s)
 
@@ -78,9 +116,14 @@ def test_fp6_weight_relayout(dev):
     n, k = 64, 512
     w = weights_f16(n, k, 41)
     c, s, _ = oracle.quantize_matrix(w, 6, clip=True)
-    c6, ts = ops.relayout_w4a4_fp6(_dev(c, dev), _h(s, dev))
-    np.testing.assert_array_equal(decode_fp6_tiles(c6.cpu().numpy(), n, k), unpack_nibbles(c))
+    c6, ts = ops.relayout_w4a4_fp6(_dev(c, dev), _h(s, dev), want_scales=True)
+    buf = c6.cpu().numpy()
+    np.testing.assert_array_equal(decode_fp6_tiles(buf, n, k), unpack_nibbles(c))
+    np.testing.assert_array_equal(fp6_scales(buf, n, k), s)
     np.testing.assert_array_equal(_u16(ts).reshape(n, k // 64), tiled_scales(s, n))
+    c6b, none = ops.relayout_w4a4_fp6(_dev(c, dev), _h(s, dev))
+    assert none is None
+    np.testing.assert_array_equal(c6b.cpu().numpy(), buf)
 
 
 # Shapes cover every tile configuration the dispatcher picks: single-wave
@@ -95,9 +138,9 @@ def test_fp6_gemm_bit_exact(dev, m, n, k):
     w = weights_f16(n, k, 501 + n)
     ac, as_ = oracle.quantize_activations(x)
     wc, ws, _ = oracle.quantize_matrix(w, 6, clip=True)
-    a6, sa = ops.quantize_activations_fp6(_dev(x, dev))
-    w6, sw = ops.relayout_w4a4_fp6(_dev(wc, dev), _h(ws, dev))
-    got = ops.w4a4_gemm_fp6(a6, sa, w6, sw, m).cpu().numpy()
+    a6, _ = ops.quantize_activations_fp6(_dev(x, dev))
+    w6, _ = ops.relayout_w4a4_fp6(_dev(wc, dev), _h(ws, dev))
+    got = ops.w4a4_gemm_fp6(a6, w6, m).cpu().numpy()
     want = oracle.w4a4_gemm(ac, as_, wc, ws)
     np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
 
@@ -113,14 +156,15 @@ def test_fp6_group_partials_exact(dev):
     wc, _, _ = oracle.quantize_matrix(w, 6)
     wc[:4] = 0x77
     partials = oracle.w4a4_partials(ac, wc)
-    a6, sa = ops.quantize_activations_fp6(_dev(x, dev))
+    a6, _ = ops.quantize_activations_fp6(_dev(x, dev))
+    a6_host = a6.cpu().numpy()
     G = k // 64
     for g in range(G):
         s_act = np.zeros((m, G), np.uint16)
         s_w = np.zeros((n, G), np.uint16)
         s_act[:, g] = 0x3C00
         s_w[:, g] = 0x3C00
-        w6, sw = ops.relayout_w4a4_fp6(_dev(wc, dev), _h(s_w, dev))
-        sa_t = _h(tiled_scales(s_act, m), dev)  # m is a multiple of 32
-        got = ops.w4a4_gemm_fp6(a6, sa_t, w6, sw, m).cpu().numpy()
+        w6, _ = ops.relayout_w4a4_fp6(_dev(wc, dev), _h(s_w, dev))
+        a6_g = _dev(set_fp6_scales(a6_host, m, k, s_act), dev)  # m is a multiple of 32
+        got = ops.w4a4_gemm_fp6(a6_g, w6, m).cpu().numpy()
         np.testing.assert_array_equal(got, partials[:, :, g].astype(np.float32))
