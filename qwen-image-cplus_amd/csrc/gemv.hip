@@ -128,7 +128,9 @@ __global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_kernel(
 //   y += s (P - 1024 X) + min X,  P = sum_k x_k (1024 + c_k),  X = sum_k x_k
 // The codes enter the matrix core as the exact fp16 integers 1024 + c (a
 // bit-field insert into 0x6400, no multiply), P is exact per product and
-// summed in fp32, and X is summed once per workgroup from the staged rows.
+// summed in fp32.  -1024 X comes from the matrix core too: two MFMAs with a
+// constant -1024 weight operand start the group's accumulator, which the
+// code MFMAs then add P onto, so no separate pass over x is needed.
 // This is the group's dot product with the weights c s + min kept in fp32,
 // instead of first rounding every weight to fp16 as the reference's
 // dequantiser does (gemm.cu:229-230): the outputs differ from that form by
@@ -137,49 +139,48 @@ __global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_factored_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
     const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int m, int n, int k) {
     __shared__ float partial[GEMV_WAVES][16][17];
-    extern __shared__ __attribute__((aligned(16))) uint16_t xs_lds[];  // m * k fp16, then m * G fp32 sums
+    extern __shared__ __attribute__((aligned(16))) uint16_t xs_lds[];  // m * k fp16
     const int groups = k >> 6;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
     const int q = lane >> 4, r16 = lane & 15;
     const int tile = blockIdx.x;
-    float *xsum = reinterpret_cast<float *>(xs_lds + static_cast<size_t>(m) * k);
 
     const int per_wave = (groups + GEMV_WAVES - 1) / GEMV_WAVES;
     const int g_begin = wave * per_wave;
     const int g_end = min(groups, g_begin + per_wave);
     const uint8_t *cp = codes + static_cast<size_t>(tile) * groups * 512 + lane * 8;
-    // The (scale, minimum) pairs of this lane's four outputs 4q .. 4q+3.
-    const uint8_t *sp = reinterpret_cast<const uint8_t *>(scales) + static_cast<size_t>(tile) * groups * 64 + q * 16;
+    // Lane l loads the (scale, minimum) pair of output 4q + l % 4; the pairs
+    // of the lane's four outputs 4q .. 4q+3 are then its quad's four loads.
+    const uint32_t *sp =
+        reinterpret_cast<const uint32_t *>(scales) + static_cast<size_t>(tile) * groups * 16 + 4 * q + (lane & 3);
 
-    uint2 c[2][GEMV_BATCH];
-    uint4 sc[2][GEMV_BATCH];
+    // Two batches in flight cover a 3072-wide row's 12 groups per wave, so
+    // each wave's whole weight stream is requested at once.
+    constexpr int FB = 6;
+    uint2 c[2][FB];
+    uint32_t sc[2][FB];
+    // When every wave's share is whole batches (groups % 48 == 0, e.g. k =
+    // 3072), batches need no per-group bounds tests: one uniform test per
+    // batch decides whether it exists.
+    const bool whole = groups % (GEMV_WAVES * 2 * FB) == 0;
     auto load_batch = [&](int b, int g) {
+        if (whole && g >= g_end) return;
 #pragma unroll
-        for (int u = 0; u < GEMV_BATCH; ++u) {
-            if (g + u < g_end) {
+        for (int u = 0; u < FB; ++u) {
+            if (whole || g + u < g_end) {
                 const v2u t =
                     __builtin_nontemporal_load(reinterpret_cast<const v2u *>(cp + static_cast<size_t>(g + u) * 512));
                 c[b][u] = uint2{t[0], t[1]};
-                const v4u v =
-                    __builtin_nontemporal_load(reinterpret_cast<const v4u *>(sp + static_cast<size_t>(g + u) * 64));
-                sc[b][u] = uint4{v[0], v[1], v[2], v[3]};
+                sc[b][u] = __builtin_nontemporal_load(sp + static_cast<size_t>(g + u) * 16);
             }
         }
     };
     load_batch(0, g_begin);
-    load_batch(1, g_begin + GEMV_BATCH);
+    load_batch(1, g_begin + FB);
 
     const int chunks = m * k / 8;  // 16-byte chunks of x
     for (int i = threadIdx.x; i < chunks; i += GEMV_WAVES * WAVE)
         reinterpret_cast<uint4 *>(xs_lds)[i] = reinterpret_cast<const uint4 *>(x)[i];
-    __syncthreads();
-    for (int i = threadIdx.x; i < m * groups; i += GEMV_WAVES * WAVE) {
-        const uint16_t *src = xs_lds + static_cast<size_t>(i) * 64;  // row i / G, group i % G
-        float t = 0.f;
-#pragma unroll 8
-        for (int e = 0; e < 64; ++e) t += h2f(src[e]);
-        xsum[i] = t;
-    }
     __syncthreads();
 
     // B operand: lane l supplies row m = l % 16 of x, inputs 8q .. 8q + 7 of
@@ -187,13 +188,12 @@ __global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_factored_kernel(
     // feed output columns that are never stored.
     const int xr = r16 < m ? r16 : 0;
     const uint16_t *xrow = xs_lds + static_cast<size_t>(xr) * k + 8 * q;
-    const float *xs_row = xsum + static_cast<size_t>(xr) * groups;
     uint32_t magic = 0x64006400u;
     asm volatile("" : "+v"(magic));  // kept in a VGPR: lets the insert be one v_bfi_b32
 
     // yacc[r] = y[m = l % 16][n = 16 tile + 4q + r] over this wave's groups.
     float yacc[4] = {0.f, 0.f, 0.f, 0.f};
-    auto consume = [&](int g, uint2 cc, uint4 scs) {
+    auto consume = [&](int g, uint2 cc, uint32_t scq) {
         // Bit-field insert of each nibble pair into 0x6400 (written in C, not
         // inline asm: these values feed the matrix core directly, and only
         // compiler-visible instructions get the VALU-to-MFMA wait states).
@@ -207,29 +207,40 @@ __global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_factored_kernel(
         const uint4 x1 = *reinterpret_cast<const uint4 *>(xrow + g * 64 + 32);
         // The nibble slot order of the tiled codes puts element 2i in nibble
         // i and 2i+1 in nibble 4+i, so a[i] holds elements (2i, 2i+1).
+        // p = -1024 X (every output row of the constant operand is alike),
+        // then P - 1024 X.
+        const uint4 neg1024 = {0xE400E400u, 0xE400E400u, 0xE400E400u, 0xE400E400u};
         v4f p = {0.f, 0.f, 0.f, 0.f};
+        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, neg1024), __builtin_bit_cast(v8h, x0), p,
+                                                   0, 0, 0);
+        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, neg1024), __builtin_bit_cast(v8h, x1), p,
+                                                   0, 0, 0);
+        const float X = p[0] * (-1.0f / 1024.0f);  // exact
         p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, uint4{a[0], a[1], a[2], a[3]}),
                                                    __builtin_bit_cast(v8h, x0), p, 0, 0, 0);
         p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, uint4{a[4], a[5], a[6], a[7]}),
                                                    __builtin_bit_cast(v8h, x1), p, 0, 0, 0);
-        const float X = xs_row[g];
-        const uint32_t sm4[4] = {scs.x, scs.y, scs.z, scs.w};
+        // Quad broadcasts (DPP quad_perm r,r,r,r) gather the four pairs.
+        const uint32_t sm4[4] = {
+            static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(scq), 0x00, 0xF, 0xF, false)),
+            static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(scq), 0x55, 0xF, 0xF, false)),
+            static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(scq), 0xAA, 0xF, 0xF, false)),
+            static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(scq), 0xFF, 0xF, 0xF, false))};
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float t = __builtin_fmaf(-1024.0f, X, p[r]);
-            yacc[r] = __builtin_fmaf(h2f(static_cast<uint16_t>(sm4[r] & 0xFFFFu)), t, yacc[r]);
+            yacc[r] = __builtin_fmaf(h2f(static_cast<uint16_t>(sm4[r] & 0xFFFFu)), p[r], yacc[r]);
             yacc[r] = __builtin_fmaf(h2f(static_cast<uint16_t>(sm4[r] >> 16)), X, yacc[r]);
         }
     };
-    for (int g = g_begin; g < g_end; g += 2 * GEMV_BATCH) {
+    for (int g = g_begin; g < g_end; g += 2 * FB) {
 #pragma unroll
-        for (int u = 0; u < GEMV_BATCH; ++u)
-            if (g + u < g_end) consume(g + u, c[0][u], sc[0][u]);
-        load_batch(0, g + 2 * GEMV_BATCH);
+        for (int u = 0; u < FB; ++u)
+            if (whole || g + u < g_end) consume(g + u, c[0][u], sc[0][u]);
+        load_batch(0, g + 2 * FB);
 #pragma unroll
-        for (int u = 0; u < GEMV_BATCH; ++u)
-            if (g + GEMV_BATCH + u < g_end) consume(g + GEMV_BATCH + u, c[1][u], sc[1][u]);
-        load_batch(1, g + 3 * GEMV_BATCH);
+        for (int u = 0; u < FB; ++u)
+            if (whole || g + FB + u < g_end) consume(g + FB + u, c[1][u], sc[1][u]);
+        load_batch(1, g + 3 * FB);
     }
 
 #pragma unroll
@@ -250,7 +261,7 @@ __global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_factored_kernel(
 static void launch_gemv(const uint16_t *x, const uint8_t *c, const uint16_t *s, const float *bias, void *y,
                         int out_type, int epi, int m, int n, int k, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(n / 16)), block(GEMV_WAVES * WAVE);
-    const long long lds = static_cast<long long>(m) * k * 2 + static_cast<long long>(m) * (k / 64) * 4;
+    const long long lds = static_cast<long long>(m) * k * 2;
     if (lds <= GEMV_LDS_X)
         w4a16_gemv_factored_kernel<<<grid, block, static_cast<size_t>(lds), stream>>>(x, c, s, bias, y, out_type, epi,
                                                                                       m, n, k);
