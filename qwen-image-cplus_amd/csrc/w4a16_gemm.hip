@@ -257,41 +257,84 @@ __global__ __launch_bounds__(NW *WAVE, 2) void w4a16_tiled_kernel(
 #pragma unroll
         for (int i = 0; i < TM; ++i) acc[j][i] = v4f{0.f, 0.f, 0.f, 0.f};
 
+    // Step st's activation fragments of row tiles 0 .. TM-1.
+    auto read_x = [&](int slot, int st, v8h (&xf)[TM]) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int row = 16 * i + r16;
+            const int chunk = (4 * st + q) ^ (row & 7);
+            xf[i] = *reinterpret_cast<const v8h *>(&lds_a[slot][row][chunk * 16]);
+        }
+    };
+    // Step 0's weights are dequantised first; step 1's one output word (two
+    // weights) at a time between step 0's MFMAs, so the vector unit works
+    // while the matrix core does (the scheduling fences keep that order).
+    // Words come from packed fp16 (and-or to 1024 + c, one packed fma) when
+    // that is provably the reference's value for every group of the wave;
+    // otherwise a rare uniform branch replaces them with the reference's fp32
+    // fma + RNE before they are used.
     auto compute = [&](int slot) {
-        // Dequantise this wave's weight fragments for both K-steps.
-        v8h wf[2][TN];
         bool fast = true;
 #pragma unroll
         for (int j = 0; j < TN; ++j)
             fast = fast && w4a16_single_rounding_exact(s_ring[slot][j] & 0xFFFFu, s_ring[slot][j] >> 16);
-        // One wave-uniform choice: the packed path unless some lane's group
-        // needs the fp32 path.
         fast = __all(fast);
+        const v2h k1024 = v2h{static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+        uint32_t magic = 0x64006400u;
+        asm volatile("" : "+v"(magic));
+        v2h s2[TN], m2[TN];
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             const uint32_t sb = s_ring[slot][j] & 0xFFFFu, mb = s_ring[slot][j] >> 16;
-            wf[0][j] = __builtin_bit_cast(v8h, w4a16_dequant8(static_cast<uint32_t>(c_ring[slot][j][0]), sb, mb, fast));
-            wf[1][j] = __builtin_bit_cast(v8h, w4a16_dequant8(static_cast<uint32_t>(c_ring[slot][j][1]), sb, mb, fast));
+            s2[j] = __builtin_bit_cast(v2h, sb | (sb << 16));
+            m2[j] = __builtin_bit_cast(v2h, mb | (mb << 16));
         }
+        // Word i of code dword `half` of tile j: nibbles i and 4 + i.
+        auto word = [&](int j, int half, int i) -> uint32_t {
+            const uint32_t x = static_cast<uint32_t>(c_ring[slot][j][half]);
+            const uint32_t biased = ((x >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu);
+            const v2h c = __builtin_bit_cast(v2h, biased) - k1024;
+            return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, s2[j], m2[j]));
+        };
+        auto exact_words = [&](int half, uint32_t (&w)[TN][4]) {
 #pragma unroll
-        for (int st = 0; st < 2; ++st) {
-            // All of this step's activation fragments first (TM LDS reads in
-            // flight), then the TM x TN MFMAs.
-            v8h xf[TM];
-#pragma unroll
-            for (int i = 0; i < TM; ++i) {
-                const int row = 16 * i + r16;
-                const int chunk = (4 * st + q) ^ (row & 7);
-                xf[i] = *reinterpret_cast<const v8h *>(&lds_a[slot][row][chunk * 16]);
+            for (int j = 0; j < TN; ++j) {
+                const uint4 e = w4a16_dequant8(static_cast<uint32_t>(c_ring[slot][j][half]), s_ring[slot][j] & 0xFFFFu,
+                                               s_ring[slot][j] >> 16, false);
+                w[j][0] = e.x;
+                w[j][1] = e.y;
+                w[j][2] = e.z;
+                w[j][3] = e.w;
             }
+        };
+        uint32_t w0[TN][4], w1[TN][4];
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[st][j], xf[i], acc[j][i], 0, 0, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, TM, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
+            for (int i = 0; i < 4; ++i) w0[j][i] = word(j, 0, i);
+        if (!fast) exact_words(0, w0);
+        v8h xf[TM];
+        read_x(slot, 0, xf);
+        __builtin_amdgcn_sched_barrier(0);
+        constexpr int NMF = TM * TN, NWD = 4 * TN;
+#pragma unroll
+        for (int t = 0; t < NMF; ++t) {
+            const int i = t / TN, j = t % TN;
+            acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                __builtin_bit_cast(v8h, uint4{w0[j][0], w0[j][1], w0[j][2], w0[j][3]}), xf[i], acc[j][i], 0, 0, 0);
+            // Words [t NWD / NMF, (t + 1) NWD / NMF) of step 1 go here.
+#pragma unroll
+            for (int wd = t * NWD / NMF; wd < (t + 1) * NWD / NMF; ++wd) w1[wd / 4][wd % 4] = word(wd / 4, 1, wd % 4);
+            __builtin_amdgcn_sched_barrier(0);
         }
+        if (!fast) exact_words(1, w1);
+        read_x(slot, 1, xf);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(v8h, uint4{w1[j][0], w1[j][1], w1[j][2], w1[j][3]}), xf[i], acc[j][i], 0, 0, 0);
     };
 
     // Prologue: groups 0 .. NSTAGE-2 in flight.  Loads are issued

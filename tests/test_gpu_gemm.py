@@ -254,3 +254,28 @@ def test_w4a16_dequant_bit_exact_identity(dev, path):
             m64 = np.repeat(mins.view(np.float16).astype(np.float64), 64, axis=1)
             want = (nib * s64 + m64).astype(np.float32)
     np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("mixed", [False, True])
+def test_w4a16_dequant_bit_exact_large_tiles(dev, mixed):
+    """The large-M tile shape (m > 1024, n % 192 == 0): x repeats the
+    identity, so every output is one dequantised weight, compared bit for bit
+    on double-rounding (scale, minimum) pairs -- in every group, or mixed with
+    ordinary groups so both dequantisation paths run in one launch."""
+    import qwen_image_hip.ops as ops
+    n, k, m = 192, 128, 1152
+    G = k // 64
+    s_adv, m_adv = _double_rounding_cases(n * G, seed=5)
+    scales = s_adv.reshape(n, G).copy()
+    mins = m_adv.reshape(n, G).copy()
+    if mixed:
+        g = np.random.default_rng(6)
+        plain = g.random((n, G)) < 0.5
+        scales[plain] = (g.random(plain.sum()) * 0.01 + 0.001).astype(np.float16).view(np.uint16)
+        mins[plain] = (-(g.random(plain.sum()) * 0.05)).astype(np.float16).view(np.uint16)
+    codes = np.random.default_rng(7).integers(0, 256, size=(n, k // 2), dtype=np.uint8)
+    want = oracle.w4a16_dequantize(codes, scales, mins).view(np.float16).astype(np.float32)   # [n, k]
+    x = np.tile(np.eye(k, dtype=np.float16), (m // k, 1))
+    tc, ts = ops.relayout_w4a16(_dev(codes, dev), _h(scales, dev), _h(mins, dev))
+    got = ops.w4a16_gemm(_dev(x, dev), tc, ts).cpu().numpy()                                  # [m, n]
+    np.testing.assert_array_equal(got.view(np.uint32), np.tile(want.T, (m // k, 1)).view(np.uint32))
