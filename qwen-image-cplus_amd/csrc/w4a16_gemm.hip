@@ -165,6 +165,90 @@ __global__ __launch_bounds__(WM *WAVE) void w4a16_gemm_kernel(
         }
 }
 
+// One 64-group of a wave's W4A16 tile: dequantise its TN weight tiles (code
+// dword pairs c[j], (scale, minimum) words sc[j]) and multiply them with the
+// TM activation row tiles staged at xs ([TM * 16][128] bytes, the 16-byte
+// chunks of row r XOR-swizzled by r & 7) into acc.
+//
+// Step 0's weights are dequantised first; step 1's one output word (two
+// weights) at a time between step 0's MFMAs, so the vector unit works while
+// the matrix core does (the scheduling fences keep that order).  Words come
+// from packed fp16 (and-or to 1024 + c, one packed fma) when that is provably
+// the reference's value for every group of the wave; otherwise a rare
+// uniform branch replaces them with the reference's fp32 fma + RNE before
+// they are used.
+template <int TM, int TN>
+__device__ __forceinline__ void w4a16_group_mfma(const uint8_t *xs, const v2i (&c)[TN], const uint32_t (&sc)[TN],
+                                                 int r16, int q, v4f (&acc)[TN][TM]) {
+    auto read_x = [&](int st, v8h(&xf)[TM]) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int row = 16 * i + r16;
+            const int chunk = (4 * st + q) ^ (row & 7);
+            xf[i] = *reinterpret_cast<const v8h *>(xs + row * 128 + chunk * 16);
+        }
+    };
+    bool fast = true;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fast = fast && w4a16_single_rounding_exact(sc[j] & 0xFFFFu, sc[j] >> 16);
+    fast = __all(fast);
+    const v2h k1024 = v2h{static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+    uint32_t magic = 0x64006400u;
+    asm volatile("" : "+v"(magic));
+    v2h s2[TN], m2[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const uint32_t sb = sc[j] & 0xFFFFu, mb = sc[j] >> 16;
+        s2[j] = __builtin_bit_cast(v2h, sb | (sb << 16));
+        m2[j] = __builtin_bit_cast(v2h, mb | (mb << 16));
+    }
+    // Word i of code dword `half` of tile j: nibbles i and 4 + i.
+    auto word = [&](int j, int half, int i) -> uint32_t {
+        const uint32_t x = static_cast<uint32_t>(c[j][half]);
+        const uint32_t biased = ((x >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu);
+        const v2h cc = __builtin_bit_cast(v2h, biased) - k1024;
+        return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(cc, s2[j], m2[j]));
+    };
+    auto exact_words = [&](int half, uint32_t(&w)[TN][4]) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const uint4 e = w4a16_dequant8(static_cast<uint32_t>(c[j][half]), sc[j] & 0xFFFFu, sc[j] >> 16, false);
+            w[j][0] = e.x;
+            w[j][1] = e.y;
+            w[j][2] = e.z;
+            w[j][3] = e.w;
+        }
+    };
+    uint32_t w0[TN][4], w1[TN][4];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w0[j][i] = word(j, 0, i);
+    if (!fast) exact_words(0, w0);
+    v8h xf[TM];
+    read_x(0, xf);
+    __builtin_amdgcn_sched_barrier(0);
+    constexpr int NMF = TM * TN, NWD = 4 * TN;
+#pragma unroll
+    for (int t = 0; t < NMF; ++t) {
+        const int i = t / TN, j = t % TN;
+        acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            __builtin_bit_cast(v8h, uint4{w0[j][0], w0[j][1], w0[j][2], w0[j][3]}), xf[i], acc[j][i], 0, 0, 0);
+        // Words [t NWD / NMF, (t + 1) NWD / NMF) of step 1 go here.
+#pragma unroll
+        for (int wd = t * NWD / NMF; wd < (t + 1) * NWD / NMF; ++wd) w1[wd / 4][wd % 4] = word(wd / 4, 1, wd % 4);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (!fast) exact_words(1, w1);
+    read_x(1, xf);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+            acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                __builtin_bit_cast(v8h, uint4{w1[j][0], w1[j][1], w1[j][2], w1[j][3]}), xf[i], acc[j][i], 0, 0, 0);
+}
+
 // ---------------------------------------------------------------------------
 // Tiled-weight kernel.
 //
@@ -257,84 +341,8 @@ __global__ __launch_bounds__(NW *WAVE, 2) void w4a16_tiled_kernel(
 #pragma unroll
         for (int i = 0; i < TM; ++i) acc[j][i] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    // Step st's activation fragments of row tiles 0 .. TM-1.
-    auto read_x = [&](int slot, int st, v8h (&xf)[TM]) {
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            const int row = 16 * i + r16;
-            const int chunk = (4 * st + q) ^ (row & 7);
-            xf[i] = *reinterpret_cast<const v8h *>(&lds_a[slot][row][chunk * 16]);
-        }
-    };
-    // Step 0's weights are dequantised first; step 1's one output word (two
-    // weights) at a time between step 0's MFMAs, so the vector unit works
-    // while the matrix core does (the scheduling fences keep that order).
-    // Words come from packed fp16 (and-or to 1024 + c, one packed fma) when
-    // that is provably the reference's value for every group of the wave;
-    // otherwise a rare uniform branch replaces them with the reference's fp32
-    // fma + RNE before they are used.
     auto compute = [&](int slot) {
-        bool fast = true;
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-            fast = fast && w4a16_single_rounding_exact(s_ring[slot][j] & 0xFFFFu, s_ring[slot][j] >> 16);
-        fast = __all(fast);
-        const v2h k1024 = v2h{static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
-        uint32_t magic = 0x64006400u;
-        asm volatile("" : "+v"(magic));
-        v2h s2[TN], m2[TN];
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const uint32_t sb = s_ring[slot][j] & 0xFFFFu, mb = s_ring[slot][j] >> 16;
-            s2[j] = __builtin_bit_cast(v2h, sb | (sb << 16));
-            m2[j] = __builtin_bit_cast(v2h, mb | (mb << 16));
-        }
-        // Word i of code dword `half` of tile j: nibbles i and 4 + i.
-        auto word = [&](int j, int half, int i) -> uint32_t {
-            const uint32_t x = static_cast<uint32_t>(c_ring[slot][j][half]);
-            const uint32_t biased = ((x >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu);
-            const v2h c = __builtin_bit_cast(v2h, biased) - k1024;
-            return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, s2[j], m2[j]));
-        };
-        auto exact_words = [&](int half, uint32_t (&w)[TN][4]) {
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const uint4 e = w4a16_dequant8(static_cast<uint32_t>(c_ring[slot][j][half]), s_ring[slot][j] & 0xFFFFu,
-                                               s_ring[slot][j] >> 16, false);
-                w[j][0] = e.x;
-                w[j][1] = e.y;
-                w[j][2] = e.z;
-                w[j][3] = e.w;
-            }
-        };
-        uint32_t w0[TN][4], w1[TN][4];
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) w0[j][i] = word(j, 0, i);
-        if (!fast) exact_words(0, w0);
-        v8h xf[TM];
-        read_x(slot, 0, xf);
-        __builtin_amdgcn_sched_barrier(0);
-        constexpr int NMF = TM * TN, NWD = 4 * TN;
-#pragma unroll
-        for (int t = 0; t < NMF; ++t) {
-            const int i = t / TN, j = t % TN;
-            acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                __builtin_bit_cast(v8h, uint4{w0[j][0], w0[j][1], w0[j][2], w0[j][3]}), xf[i], acc[j][i], 0, 0, 0);
-            // Words [t NWD / NMF, (t + 1) NWD / NMF) of step 1 go here.
-#pragma unroll
-            for (int wd = t * NWD / NMF; wd < (t + 1) * NWD / NMF; ++wd) w1[wd / 4][wd % 4] = word(wd / 4, 1, wd % 4);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if (!fast) exact_words(1, w1);
-        read_x(slot, 1, xf);
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-                acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    __builtin_bit_cast(v8h, uint4{w1[j][0], w1[j][1], w1[j][2], w1[j][3]}), xf[i], acc[j][i], 0, 0, 0);
+        w4a16_group_mfma<TM, TN>(&lds_a[slot][0][0], c_ring[slot], s_ring[slot], r16, q, acc);
     };
 
     // Prologue: groups 0 .. NSTAGE-2 in flight.  Loads are issued
@@ -397,6 +405,149 @@ static int launch_tiled(const void *x, const void *codes, const void *scales, co
     return launch_status();
 }
 
+// ---------------------------------------------------------------------------
+// K-split kernel for short M (the text stream's 256 rows).
+//
+// With few rows the grid is small and a tile's 64-groups run one after
+// another, so the tiled kernel is latency-bound.  Here the four wavefronts of
+// a workgroup share one BM x BN output tile and each streams a contiguous
+// quarter of the groups through its own LDS ring (no barrier in the loop);
+// the four partial tiles are then added in a fixed order (wave 0 + 1 + 2 + 3)
+// through LDS, so results do not depend on timing.  Summation order differs
+// from the tiled kernel's by the K split only, inside the W4A16 tolerance.
+template <int TM, int TN>
+__global__ __launch_bounds__(4 * WAVE) void w4a16_splitk_kernel(
+    const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
+    const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int m, int n, int k) {
+    constexpr int NW = 4, NSTAGE = 4;
+    constexpr int BM = TM * 16, BN = TN * 16;
+    constexpr int A_PER_W = BM / 8;  // 1 KiB direct loads: rows 8u .. 8u+7
+    constexpr int LOADS_PER_GROUP = A_PER_W + 2 * TN;
+    constexpr int RING = NSTAGE * BM * 128;  // bytes per wave
+    static_assert(BM * BN * 4 <= RING, "a wave's partial tile fits in its ring");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[NW * RING];
+
+    const int groups = k >> 6;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
+    const int q = lane >> 4, r16 = lane & 15;
+    const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
+    int tm, tn;
+    tile_of_block(blockIdx.x, tiles_m, tiles_n, 8, tm, tn);
+    const int block_row = tm * BM, block_col = tn * BN;
+    const int g_lo = wave * groups / NW, cnt = (wave + 1) * groups / NW - g_lo;
+    uint8_t *ring = lds + wave * RING;
+
+    const uint32_t x_bytes = static_cast<uint32_t>(m) * static_cast<uint32_t>(k) * 2u;
+    const uint32_t c_bytes = static_cast<uint32_t>(n) * static_cast<uint32_t>(k / 2);
+    const uint32_t s_bytes = static_cast<uint32_t>(n) * static_cast<uint32_t>(groups) * 4u;
+    const auto rx = buffer_rsrc(x, x_bytes);
+    const auto rc = buffer_rsrc(codes, c_bytes);
+    const auto rs = buffer_rsrc(scales, s_bytes);
+    uint32_t x_vo[A_PER_W];
+#pragma unroll
+    for (int u = 0; u < A_PER_W; ++u) {
+        const int row = 8 * u + (lane >> 3), grow = block_row + row;
+        const int chunk = (lane & 7) ^ (row & 7);
+        x_vo[u] = grow < m ? static_cast<uint32_t>(grow) * k * 2u + (g_lo * 128u) + chunk * 16u : x_bytes;
+    }
+    uint32_t c_vo[TN], s_vo[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int tile = block_col / 16 + j;
+        const bool ok = tile < n / 16;
+        c_vo[j] = ok ? (static_cast<uint32_t>(tile) * groups + g_lo) * 512u + lane * 8u : c_bytes;
+        s_vo[j] = ok ? (static_cast<uint32_t>(tile) * groups + g_lo) * 64u + r16 * 4u : s_bytes;
+    }
+
+    v2i c_ring[NSTAGE][TN];
+    uint32_t s_ring[NSTAGE][TN];
+    // Group g_lo + gi into ring slot `slot`.  Past this wave's range the loads
+    // read harmless bytes (the next groups, tile or row, or zeros past the
+    // end) into slots that are never consumed.
+    auto issue = [&](int gi, int slot) {
+#pragma unroll
+        for (int u = 0; u < A_PER_W; ++u) buffer_load_lds16(rx, ring + (slot * BM + 8 * u) * 128, x_vo[u], gi * 128);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            c_ring[slot][j] = __builtin_amdgcn_raw_buffer_load_b64(rc, c_vo[j], gi * 512, 0);
+            s_ring[slot][j] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, s_vo[j], gi * 64, 0));
+        }
+    };
+
+    v4f acc[TN][TM];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int i = 0; i < TM; ++i) acc[j][i] = v4f{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int p = 0; p < NSTAGE - 1; ++p) issue(p, p);
+    for (int g0 = 0; g0 < cnt; g0 += NSTAGE) {
+#pragma unroll
+        for (int u = 0; u < NSTAGE; ++u) {
+            const int gi = g0 + u;
+            // Only this wave reads its ring, so completing its own loads is
+            // enough: no workgroup barrier.  The slot refilled next was last
+            // read by this wave's previous group, whose reads have completed
+            // (their values fed that group's MFMAs).
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTAGE - 2) * LOADS_PER_GROUP) : "memory");
+            issue(gi + NSTAGE - 1, (u + NSTAGE - 1) % NSTAGE);
+            if (gi < cnt) w4a16_group_mfma<TM, TN>(ring + u * BM * 128, c_ring[u], s_ring[u], r16, q, acc);
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // Partial tiles through LDS, each wave into its own ring, then summed in
+    // wave order: position ((j * TM + i) * 64 + lane) holds acc[j][i].
+    __syncthreads();
+    float4 *part = reinterpret_cast<float4 *>(ring);
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+            part[(j * TM + i) * WAVE + lane] = float4{acc[j][i][0], acc[j][i][1], acc[j][i][2], acc[j][i][3]};
+    __syncthreads();
+    for (int pos = threadIdx.x; pos < TN * TM * WAVE; pos += NW * WAVE) {
+        float4 v = reinterpret_cast<const float4 *>(lds)[pos];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            const float4 t = reinterpret_cast<const float4 *>(lds + w * RING)[pos];
+            v.x += t.x;
+            v.y += t.y;
+            v.z += t.z;
+            v.w += t.w;
+        }
+        // acc[j][i][r] = y[row, col]: row = m-tile i, lane % 16; col = n-tile
+        // j, 4 (lane / 16) + r.
+        const int ln = pos % WAVE, ji = pos / WAVE, i = ji % TM, j = ji / TM;
+        const int row = block_row + 16 * i + (ln & 15), col = block_col + 16 * j + 4 * (ln >> 4);
+        if (row >= m || col >= n) continue;
+        const float vv[4] = {epilogue(v.x, bias, col, epi), epilogue(v.y, bias, col + 1, epi),
+                             epilogue(v.z, bias, col + 2, epi), epilogue(v.w, bias, col + 3, epi)};
+        const size_t idx = static_cast<size_t>(row) * n + col;
+        if (out_type == QI_HIP_OUT_F16) {
+            uint2 h;
+            h.x = static_cast<uint32_t>(f2h(vv[0])) | (static_cast<uint32_t>(f2h(vv[1])) << 16);
+            h.y = static_cast<uint32_t>(f2h(vv[2])) | (static_cast<uint32_t>(f2h(vv[3])) << 16);
+            *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(y) + idx) = h;
+        } else {
+            *reinterpret_cast<float4 *>(reinterpret_cast<float *>(y) + idx) = float4{vv[0], vv[1], vv[2], vv[3]};
+        }
+    }
+}
+
+template <int TM, int TN>
+static int launch_splitk(const void *x, const void *codes, const void *scales, const float *bias, void *y,
+                         int out_type, int epi, int m, int n, int k, hipStream_t stream) {
+    constexpr int BM = TM * 16, BN = TN * 16;
+    const long long blocks = static_cast<long long>((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+    if (blocks > 0x7FFFFFFFLL) return kInvalid;
+    w4a16_splitk_kernel<TM, TN><<<dim3(static_cast<unsigned>(blocks)), dim3(4 * WAVE), 0, stream>>>(
+        static_cast<const uint16_t *>(x), static_cast<const uint8_t *>(codes), static_cast<const uint16_t *>(scales),
+        bias, y, out_type, epi, m, n, k);
+    return launch_status();
+}
+
 template <int TM, int TN, int WM, bool TILED>
 static int launch(const void *x, const void *codes, const void *scales, const void *minimums, const float *bias,
                   void *y, int out_type, int epi, int m, int n, int k, hipStream_t stream) {
@@ -452,6 +603,14 @@ QI_API int qi_hip_w4a16_gemm_tiled(const void *x_half, const void *w_tiled_codes
     if (static_cast<long long>(m) * k * 2 >= (1LL << 32) || static_cast<long long>(n) * (k / 2) >= (1LL << 32))
         return kInvalid;
     // Small m: short row tiles so the grid still covers the 256 CUs.
+    // Short M with few column tiles (the text stream's 256 x 3072 outputs):
+    // the tiled grid is too small to fill the chip, so split K across the
+    // workgroup's waves instead (measured on MI355X: 256 x 3072 x 3072 20.4
+    // -> 17.5 us, 256 x 3072 x 12288 67.4 -> 49.3 us; wider N keeps the tiled
+    // kernel).
+    if (m <= 256 && static_cast<long long>((m + 31) / 32) * ((n + 63) / 64) < 1024)
+        return launch_splitk<4, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
+                                   stream_of(stream));
     if (m <= 256)
         return launch_tiled<2, 1, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
                                      stream_of(stream));

@@ -132,8 +132,10 @@ def test_w4a16_reference_abi(dev, m, n, k):
     _close(got, want)
 
 
-@pytest.mark.parametrize("m,n,k,clip", [(17, 16, 64, False), (100, 48, 192, True), (300, 512, 3584 // 64 * 64, False),
-                                        (1024, 256, 1024, True)])
+# m <= 256 with few column tiles runs the K-split kernel (17, 100, 256
+# rows here), larger m the tiled kernel.
+@pytest.mark.parametrize("m,n,k,clip", [(17, 16, 64, False), (100, 48, 192, True), (256, 192, 3072, False),
+                                        (300, 512, 3584 // 64 * 64, False), (1024, 256, 1024, True)])
 def test_w4a16_tiled(dev, m, n, k, clip):
     print(f"w4a16 tiled m={m} n={n} k={k}", flush=True)
     import qwen_image_hip.ops as ops
