@@ -143,8 +143,8 @@ int qi_hip_w4a16_gemv(const void *x_half, const void *w_tiled_codes, const void 
  *
  * Quantiser (same arithmetic and codes as qi_w4a4_quantize_activations):
  * x is f32 (x_is_half = 0) or fp16 [m, k]; codes6 holds ceil(m/32) * 32 rows
- * (rows past m are left unwritten and never stored from); k % 256 == 0;
- * codes6 4-byte aligned. */
+ * (rows past m get the codes of zeros, and the GEMM stores nothing from
+ * them); k % 256 == 0; codes6 16-byte aligned. */
 int qi_hip_w4a4_quantize_activations_fp6(const void *x, int x_is_half, void *codes6, void *scales_tiled, int m,
                                          int k, void *stream);
 /* One-time re-layout of QIPACK W4A4 weights (codes [n, k/2], scales [n, G])

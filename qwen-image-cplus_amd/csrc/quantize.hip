@@ -21,13 +21,20 @@ namespace qi {
 constexpr int QUANT_WAVES = 4;  // chunks per workgroup
 
 // The butterfly of int4_pack.cplus:263-266 / gemm.cu:33-36 in its exact
-// fp32 operation order (left-to-right sums, then * 0.5).
+// fp32 operation order (left-to-right sums, then * 0.5).  HALF = false
+// leaves out the * 0.5: scaling by a power of two commutes with every
+// rounding of the sums as long as no value overflows or turns subnormal, so
+// the four stages' factors can be applied once, as 1/16, where the values are
+// used.  That holds for fp16 inputs (every intermediate is a multiple of
+// 2^-28 and below 2^25); fp32 inputs keep the factor per stage.
+template <bool HALF>
 __device__ __forceinline__ void butterfly4(float &a, float &b, float &c, float &d) {
     const float x0 = a, x1 = b, x2 = c, x3 = d;
-    a = (x0 + x1 + x2 - x3) * 0.5f;
-    b = (x0 + x1 - x2 + x3) * 0.5f;
-    c = (x0 - x1 + x2 + x3) * 0.5f;
-    d = (-x0 + x1 + x2 + x3) * 0.5f;
+    const float f = HALF ? 0.5f : 1.0f;
+    a = (x0 + x1 + x2 - x3) * f;
+    b = (x0 + x1 - x2 + x3) * f;
+    c = (x0 - x1 + x2 + x3) * f;
+    d = (-x0 + x1 + x2 + x3) * f;
 }
 
 template <typename In>
@@ -48,13 +55,6 @@ __device__ __forceinline__ void load4<uint16_t>(const uint16_t *src, float v[4])
     v[3] = h2f(static_cast<uint16_t>(t.y >> 16));
 }
 
-// FMT 0: QIPACK activation layout (codes [m, k/2] nibbles, scales [m, k/64]).
-// FMT 1: fp6 MFMA-operand layout: per 32-row tile T and group g, 1792 bytes
-//        = half 0 (64 lanes x 16 bytes) then half 1 (64 lanes x 12 bytes);
-//        lane l of half h holds the E2M3 codes (6 bits each, little-endian)
-//        of inputs 32 * (l / 32) + 16h .. + 15 of the group, row 32T + l % 32;
-//        bytes 12..15 of a half-0 slot hold that row's fp16 scale, zero-
-//        extended.  Scales also [m/32][G][32] fp16.
 // LDS word of element i of a chunk: an XOR swizzle that makes every access
 // pattern below (4 consecutive words per lane, and the strided butterfly
 // quadruples of strides 4, 16, 64) conflict-free for 32 lanes at a time.
@@ -67,11 +67,76 @@ __device__ __forceinline__ uint32_t e2m3_of(int q) {
     return (__builtin_amdgcn_ubfe(0xFEDCA840u, 4 * a, 4) << 1) | (q < 0 ? 32u : 0u);
 }
 
-// Grid: x = row, y = group of QUANT_WAVES * CPW chunks of the row.  Wave w
-// of the workgroup owns chunks base + w + QUANT_WAVES * i, i < CPW (chunk c =
-// elements [256c, 256c + 256) of the row); it issues all their loads first
-// and reuses its LDS addressing for each.
-template <typename In, int FMT, int CPW>
+// One 256-element chunk held by a wave, lane l owning elements 4l .. 4l+3
+// (v, in place): the H256 rotation in the reference's exact fp32 operation
+// order, then the group absmax, fp16 scale and int4 codes.  Lanes 16g ..
+// 16g+15 hold group g of the chunk; every lane of a group gets its scale.
+// buf is the wave's private 256-float LDS slice.
+template <typename In>
+__device__ __forceinline__ void quantize_chunk(float (&v)[4], float *buf, int lane, int (&q)[4],
+                                               uint16_t &scale_bits) {
+    constexpr bool HALF = !__is_same(In, uint16_t);  // see butterfly4
+    butterfly4<HALF>(v[0], v[1], v[2], v[3]);  // stride 1: in registers
+#pragma unroll
+    for (int j = 0; j < 4; ++j) buf[swz(lane * 4 + j)] = v[j];
+    // The chunk belongs to this wave alone, and a wave's LDS accesses execute
+    // in order, so the stages need no barrier -- only a compiler fence.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int stride = 4; stride < 256; stride *= 4) {
+        // Lane b owns butterfly b of this stage.
+        const int i0 = (lane / stride) * (stride * 4) + (lane % stride);
+        float a = buf[swz(i0)], b = buf[swz(i0 + stride)], cc = buf[swz(i0 + 2 * stride)],
+              d = buf[swz(i0 + 3 * stride)];
+        butterfly4<HALF>(a, b, cc, d);
+        // A stage's butterflies partition the chunk, so a lane rewrites only
+        // the four elements it just read.
+        buf[swz(i0)] = a;
+        buf[swz(i0 + stride)] = b;
+        buf[swz(i0 + 2 * stride)] = cc;
+        buf[swz(i0 + 3 * stride)] = d;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = buf[swz(lane * 4 + j)];
+    // The next chunk's first writes must follow these reads.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+
+    // The rotated values are v / unit (unit = 16 without the per-stage
+    // halving, else 1; exact).  absmax is order-free.
+    constexpr float unit = HALF ? 1.0f : 16.0f;
+    float peak = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+    for (int s = 8; s > 0; s >>= 1) peak = fmaxf(peak, __shfl_xor(peak, s, 64));
+    // gemm.cu:45-48: IEEE division by 7, fp16 RNE scale, IEEE v / scale,
+    // rint (nearest even), clamp to [-7, 7].
+    scale_bits = f2h(fmaxf((peak * (1.0f / unit)) / 7.0f, 5.9604645e-08f));
+    // v / scale as one correctly rounded quotient per element, without a
+    // division each: with y = RN(1 / d) (one IEEE division per lane), q0 =
+    // RN(v y), r = v - q0 d (exact by fma) and q0 + r y rounded once give
+    // RN(v / d) (Markstein's theorem) whenever the quotient is a normal
+    // number; below 2^-126 both are 0 after rint, and a zero's sign does not
+    // survive the conversion to int.  d = unit * scale: (v / unit) / scale
+    // and v / (unit * scale) are the same real number.
+    const float d = h2f(scale_bits) * unit;
+    const float y = 1.0f / d;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float q0 = v[j] * y;
+        const float quot = __builtin_fmaf(__builtin_fmaf(-q0, d, v[j]), y, q0);
+        q[j] = static_cast<int>(fminf(fmaxf(rintf(quot), -7.0f), 7.0f));
+    }
+}
+
+// QIPACK layout (FMT 0).  Grid: x = row, y = group of QUANT_WAVES * CPW
+// chunks of the row.  Wave w of the workgroup owns chunks base + w +
+// QUANT_WAVES * i, i < CPW (chunk c = elements [256c, 256c + 256) of the
+// row); it issues all their loads first.  Each lane stores its four nibbles
+// as one 2-byte word, so a wave writes 128 contiguous bytes.
+template <typename In, int CPW>
 __global__ __launch_bounds__(QUANT_WAVES * WAVE) void quantize_chunks_kernel(
     const In *__restrict__ x, uint8_t *__restrict__ codes, uint16_t *__restrict__ scales, int k) {
     __shared__ float lds[QUANT_WAVES][256];
@@ -94,75 +159,83 @@ __global__ __launch_bounds__(QUANT_WAVES * WAVE) void quantize_chunks_kernel(
         const int c = c0 + QUANT_WAVES * i;
         if (c >= chunks_per_row) break;
         float v[4] = {in[i][0], in[i][1], in[i][2], in[i][3]};
-        butterfly4(v[0], v[1], v[2], v[3]);  // stride 1: in registers
-#pragma unroll
-        for (int j = 0; j < 4; ++j) buf[swz(lane * 4 + j)] = v[j];
-        // The chunk belongs to this wave alone, and a wave's LDS accesses
-        // execute in order, so the stages need no barrier -- only a compiler
-        // fence.
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int stride = 4; stride < 256; stride *= 4) {
-            // Lane b owns butterfly b of this stage.
-            const int i0 = (lane / stride) * (stride * 4) + (lane % stride);
-            float a = buf[swz(i0)], b = buf[swz(i0 + stride)], cc = buf[swz(i0 + 2 * stride)],
-                  d = buf[swz(i0 + 3 * stride)];
-            butterfly4(a, b, cc, d);
-            // A stage's butterflies partition the chunk, so a lane rewrites
-            // only the four elements it just read.
-            buf[swz(i0)] = a;
-            buf[swz(i0 + stride)] = b;
-            buf[swz(i0 + 2 * stride)] = cc;
-            buf[swz(i0 + 3 * stride)] = d;
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = buf[swz(lane * 4 + j)];
-        // The next chunk's first writes must follow these reads.
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-
-        // Group g of the chunk = lanes 16g .. 16g+15.  absmax is order-free.
-        float peak = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-#pragma unroll
-        for (int s = 8; s > 0; s >>= 1) peak = fmaxf(peak, __shfl_xor(peak, s, 64));
-        // gemm.cu:45-48: IEEE division by 7, fp16 RNE scale, IEEE v / scale,
-        // rint (nearest even), clamp to [-7, 7].
-        const uint16_t scale_bits = f2h(fmaxf(peak / 7.0f, 5.9604645e-08f));
-        const float scale = h2f(scale_bits);
         int q[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) q[j] = static_cast<int>(fminf(fmaxf(rintf(v[j] / scale), -7.0f), 7.0f));
+        uint16_t scale_bits;
+        quantize_chunk<In>(v, buf, lane, q, scale_bits);
         const int g = c * 4 + (lane >> 4);  // group within the row
-        if (FMT == 0) {
-            const uint16_t packed = static_cast<uint16_t>((q[0] & 0xF) | ((q[1] & 0xF) << 4) | ((q[2] & 0xF) << 8) |
-                                                          ((q[3] & 0xF) << 12));
-            reinterpret_cast<uint16_t *>(codes)[static_cast<size_t>(row) * (k >> 2) + c * 64 + lane] = packed;
-            if ((lane & 15) == 0) scales[static_cast<size_t>(row) * (k >> 6) + g] = scale_bits;
+        const uint16_t packed =
+            static_cast<uint16_t>((q[0] & 0xF) | ((q[1] & 0xF) << 4) | ((q[2] & 0xF) << 8) | ((q[3] & 0xF) << 12));
+        reinterpret_cast<uint16_t *>(codes)[static_cast<size_t>(row) * (k >> 2) + c * 64 + lane] = packed;
+        if ((lane & 15) == 0) scales[static_cast<size_t>(row) * (k >> 6) + g] = scale_bits;
+    }
+}
+
+// fp6 MFMA-operand layout (FMT 1): per 32-row tile T and group g, 1792 bytes
+// = half 0 (64 lanes x 16 bytes) then half 1 (64 lanes x 12 bytes); lane l
+// of half h holds the E2M3 codes (6 bits each, little-endian) of inputs
+// 32 * (l / 32) + 16h .. + 15 of the group, row 32T + l % 32; bytes 12..15 of
+// a half-0 slot hold that row's fp16 scale, zero-extended.  Scales also
+// [m/32][G][32] fp16 when requested.
+//
+// Grid: x = 32-row tile, y = chunk.  A workgroup quantises the tile's 32 rows
+// of one chunk -- the tile's blocks for the chunk's four groups, 7168
+// contiguous bytes -- assembling them in LDS and writing them with 16-byte
+// stores (one row per workgroup would scatter 4-byte stores of 32
+// workgroups over every block).  Wave w takes rows w * RPW .. + RPW - 1 and
+// issues all their loads first.  Rows past m quantise zeros; their codes are
+// written but never used.
+template <typename In, int RPW>
+__global__ __launch_bounds__(32 / RPW * WAVE) void quantize_fp6_strip_kernel(
+    const In *__restrict__ x, uint8_t *__restrict__ codes, uint16_t *__restrict__ scales, int m, int k) {
+    constexpr int NWV = 32 / RPW;
+    __shared__ float lds[NWV][256];
+    __shared__ __attribute__((aligned(16))) uint32_t blocks[4 * FP6_BLOCK / 4];
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int wave = threadIdx.x >> 6;
+    const int groups = k >> 6;
+    const int tile = blockIdx.x, c = blockIdx.y;
+    float *buf = lds[wave];
+
+    float in[RPW][4];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        const int row = tile * 32 + wave * RPW + i;
+        if (row < m) {
+            load4<In>(x + static_cast<size_t>(row) * k + c * 256 + lane * 4, in[i]);
         } else {
-            // This lane's four inputs are 4p..4p+3 of slice sl of group g
-            // (inputs 16 sl .. 16 sl + 15).  Slice sl goes to half sl & 1 of
-            // the (32-row tile, group) block, lane slot 32 (sl >> 1) + row %
-            // 32, whose 12 code bytes are the 24-bit runs of lanes p = 0..3:
-            // lane p < 3 assembles and stores dword p.  In half 0 (16-byte
-            // slots) lane p = 3 stores the scale as dword 3.
-            const int sl = (lane & 15) >> 2, p = lane & 3;
-            const uint32_t bits =
-                e2m3_of(q[0]) | (e2m3_of(q[1]) << 6) | (e2m3_of(q[2]) << 12) | (e2m3_of(q[3]) << 18);
-            const uint32_t next = static_cast<uint32_t>(__shfl_down(static_cast<int>(bits), 1, 64));
-            const uint32_t block = (row >> 5) * (k >> 6) + g;
-            const uint32_t r32 = row & 31, slot = (sl >> 1) * 32 + r32;
-            uint32_t *dst = reinterpret_cast<uint32_t *>(codes + static_cast<size_t>(block) * FP6_BLOCK +
-                                                         ((sl & 1) ? FP6_HALF0 + slot * 12 : slot * 16));
-            if (p < 3)
-                dst[p] = (bits >> (8 * p)) | (next << (24 - 8 * p));
-            else if ((sl & 1) == 0)
-                dst[3] = scale_bits;
-            if (scales && (lane & 15) == 0) scales[static_cast<size_t>(block) * 32 + r32] = scale_bits;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) in[i][j] = 0.f;
         }
     }
+    // This lane's four inputs are 4p..4p+3 of slice sl of its group (inputs
+    // 16 sl .. 16 sl + 15).  Slice sl goes to half sl & 1 of the group's
+    // block, lane slot 32 (sl >> 1) + row % 32, whose 12 code bytes are the
+    // 24-bit runs of lanes p = 0..3: lane p < 3 assembles and stores dword
+    // p.  In half 0 (16-byte slots) lane p = 3 stores the scale as dword 3.
+    const int sl = (lane & 15) >> 2, p = lane & 3, gb = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        float v[4] = {in[i][0], in[i][1], in[i][2], in[i][3]};
+        int q[4];
+        uint16_t scale_bits;
+        quantize_chunk<In>(v, buf, lane, q, scale_bits);
+        const int r32 = wave * RPW + i;
+        const uint32_t bits =
+            e2m3_of(q[0]) | (e2m3_of(q[1]) << 6) | (e2m3_of(q[2]) << 12) | (e2m3_of(q[3]) << 18);
+        const uint32_t next = static_cast<uint32_t>(__shfl_down(static_cast<int>(bits), 1, 64));
+        const int slot = (sl >> 1) * 32 + r32;
+        uint32_t *dst = blocks + (gb * FP6_BLOCK + ((sl & 1) ? FP6_HALF0 + slot * 12 : slot * 16)) / 4;
+        if (p < 3)
+            dst[p] = (bits >> (8 * p)) | (next << (24 - 8 * p));
+        else if ((sl & 1) == 0)
+            dst[3] = scale_bits;
+        if (scales && (lane & 15) == 0)
+            scales[(static_cast<size_t>(tile) * groups + c * 4 + gb) * 32 + r32] = scale_bits;
+    }
+    __syncthreads();
+    uint4 *out = reinterpret_cast<uint4 *>(codes + (static_cast<size_t>(tile) * groups + c * 4) * FP6_BLOCK);
+    for (int idx = threadIdx.x; idx < 4 * FP6_BLOCK / 16; idx += NWV * WAVE)
+        out[idx] = reinterpret_cast<const uint4 *>(blocks)[idx];
 }
 
 __global__ void f32_to_f16_kernel(const float *__restrict__ src, uint16_t *__restrict__ out,
@@ -189,26 +262,40 @@ static int launch_quantize(const In *x, void *codes, void *scales, int m, int k,
     // scale array is optional (null: not written).
     if (m < 0 || k <= 0 || k % 256 != 0 || (m > 0 && (!x || !codes || (FMT == 0 && !scales)))) return kInvalid;
     if (m == 0) return 0;
-    // Vector loads: 4 elements per lane; 2-byte (QIPACK) or 4-byte (fp6) code stores.
+    // Vector loads: 4 elements per lane; 2-byte (QIPACK) or 16-byte (fp6)
+    // code stores.
     if (reinterpret_cast<uintptr_t>(x) % (4 * sizeof(In)) != 0 ||
-        reinterpret_cast<uintptr_t>(codes) % (FMT == 0 ? 2 : 4) != 0 ||
+        reinterpret_cast<uintptr_t>(codes) % (FMT == 0 ? 2 : 16) != 0 ||
         reinterpret_cast<uintptr_t>(scales) % 2 != 0)
         return kInvalid;
-    // Several chunks per wave when there are rows enough to fill the chip.
     const int chunks = k / 256;
+    if (FMT == 1) {
+        if (chunks > 65535) return kInvalid;
+        const dim3 grid(static_cast<unsigned>((m + 31) / 32), static_cast<unsigned>(chunks));
+        // Eight rows per wave when there are rows enough to fill the chip,
+        // else two (16 waves per workgroup).
+        if (m >= 1024)
+            quantize_fp6_strip_kernel<In, 8><<<grid, dim3(4 * WAVE), 0, stream>>>(
+                x, static_cast<uint8_t *>(codes), static_cast<uint16_t *>(scales), m, k);
+        else
+            quantize_fp6_strip_kernel<In, 2><<<grid, dim3(16 * WAVE), 0, stream>>>(
+                x, static_cast<uint8_t *>(codes), static_cast<uint16_t *>(scales), m, k);
+        return launch_status();
+    }
+    // Several chunks per wave when there are rows enough to fill the chip.
     if (m >= 1024) {
         constexpr int CPW = 4;
         const int chunk_groups = (chunks + QUANT_WAVES * CPW - 1) / (QUANT_WAVES * CPW);
         if (chunk_groups > 65535) return kInvalid;
-        quantize_chunks_kernel<In, FMT, CPW><<<dim3(static_cast<unsigned>(m), chunk_groups), dim3(QUANT_WAVES * WAVE),
-                                               0, stream>>>(x, static_cast<uint8_t *>(codes),
-                                                            static_cast<uint16_t *>(scales), k);
+        quantize_chunks_kernel<In, CPW><<<dim3(static_cast<unsigned>(m), chunk_groups), dim3(QUANT_WAVES * WAVE), 0,
+                                          stream>>>(x, static_cast<uint8_t *>(codes), static_cast<uint16_t *>(scales),
+                                                    k);
     } else {
         const int chunk_groups = (chunks + QUANT_WAVES - 1) / QUANT_WAVES;
         if (chunk_groups > 65535) return kInvalid;
-        quantize_chunks_kernel<In, FMT, 1><<<dim3(static_cast<unsigned>(m), chunk_groups), dim3(QUANT_WAVES * WAVE), 0,
-                                             stream>>>(x, static_cast<uint8_t *>(codes),
-                                                       static_cast<uint16_t *>(scales), k);
+        quantize_chunks_kernel<In, 1><<<dim3(static_cast<unsigned>(m), chunk_groups), dim3(QUANT_WAVES * WAVE), 0,
+                                        stream>>>(x, static_cast<uint8_t *>(codes), static_cast<uint16_t *>(scales),
+                                                  k);
     }
     return launch_status();
 }
