@@ -111,6 +111,33 @@ def test_fp6_quantizer_matches_codes(dev, m, k, half):
     np.testing.assert_array_equal(got_s[:m], want_s)
 
 
+@pytest.mark.parametrize("half", [False, True])
+def test_quantizers_round_exact_ties(dev, half):
+    """Rows alpha e_i + beta e_j with alpha = 60 + 8t, beta = 52 - 8t rotate
+    (H256, exact in fp32) to +-7 and +-(t + 0.5): the group scale is exactly
+    1 and every other value is an exact rint tie, so both quantisers' division
+    and rounding (to even) are compared bit for bit with the oracle where a
+    quotient one ulp off would change the code."""
+    import qwen_image_hip.ops as ops
+    m, k = 64, 512
+    x = np.zeros((m, k), np.float32)
+    g = np.random.default_rng(91)
+    for r in range(m):
+        t = r % 7
+        c = g.integers(0, k // 256)
+        i, j = g.choice(256, 2, replace=False)
+        x[r, c * 256 + i] = 60 + 8 * t
+        x[r, c * 256 + j] = (52 - 8 * t) * (1 if r % 2 else -1)
+    xin = x.astype(np.float16) if half else x
+    want_c, want_s = oracle.quantize_activations(xin.view(np.uint16) if half else xin)
+    c6, _ = ops.quantize_activations_fp6(_dev(xin, dev))
+    np.testing.assert_array_equal(decode_fp6_tiles(c6.cpu().numpy(), m, k), unpack_nibbles(want_c))
+    np.testing.assert_array_equal(fp6_scales(c6.cpu().numpy(), m, k), want_s)
+    c4, s4 = ops.quantize_activations(_dev(xin, dev))
+    np.testing.assert_array_equal(c4.cpu().numpy(), want_c)
+    np.testing.assert_array_equal(_u16(s4), want_s)
+
+
 def test_fp6_weight_relayout(dev):
     import qwen_image_hip.ops as ops
     n, k = 64, 512
