@@ -120,9 +120,16 @@ __device__ __forceinline__ uint4 w4a16_dequant8(uint32_t x, uint32_t scale_bits,
     return uint4{out[0], out[1], out[2], out[3]};
 }
 
-// ops.cu:156-160 (gelu_tanh_kernel) formula, evaluated in fp32.
+// The tanh-form GELU of ops.cu:156-160 (gelu_tanh_kernel),
+//   0.5 v (1 + tanh(u)),  u = sqrt(2 / pi) (v + 0.044715 v^3),
+// through the logistic identity 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)):
+// v / (1 + 2^(c t)) with t = v (1 + 0.044715 v^2) and c = -2 sqrt(2 / pi)
+// log2(e), on the hardware exp2 and reciprocal (a few ulp in fp32; the
+// outputs are compared within the fp16 output tolerance).  Large |v| are
+// safe: 2^(c t) goes to +inf (v -> -0) or to 0 (v -> v).
 __device__ __forceinline__ float gelu_tanh(float v) {
-    return 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+    const float t = v * __builtin_fmaf(0.044715f * v, v, 1.0f);
+    return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-2.3022082f * t));
 }
 
 __device__ __forceinline__ float wave_max(float v) {

@@ -146,6 +146,25 @@ def test_w4a16_tiled(dev, m, n, k, clip):
     _close(got, want)
 
 
+def test_gelu_epilogue_accuracy(dev):
+    """The fused GELU on outputs spanning [-12, 12] (x = identity, so each
+    output is one dequantised weight), fp32 out, against the oracle's tanhf
+    form: within a few fp32 ulp of max(1, |v|)."""
+    import qwen_image_hip.ops as ops
+    n, k = 128, 128
+    g = np.random.default_rng(17)
+    codes = g.integers(0, 256, size=(n, k // 2), dtype=np.uint8)
+    scales = np.full((n, k // 64), 1.6, np.float16).view(np.uint16)
+    mins = (g.random((n, k // 64)) * 12.0 - 12.0).astype(np.float16).view(np.uint16)
+    w = oracle.w4a16_dequantize(codes, scales, mins).view(np.float16).astype(np.float32)   # [n, k]
+    tc, ts = ops.relayout_w4a16(_dev(codes, dev), _h(scales, dev), _h(mins, dev))
+    got = ops.w4a16_gemm(_dev(np.eye(k, dtype=np.float16), dev), tc, ts, gelu=True).cpu().numpy()  # [k, n]
+    want = oracle.gelu_tanh(w.T)
+    err = np.abs(got - want) / np.maximum(1.0, np.abs(w.T))
+    assert w.min() < -11 and w.max() > 11
+    assert err.max() <= 4e-6, err.max()
+
+
 @pytest.mark.parametrize("gelu", [False, True])
 def test_w4a16_epilogue_f16_bias_gelu(dev, gelu):
     import qwen_image_hip.ops as ops
