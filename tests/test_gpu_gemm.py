@@ -277,14 +277,15 @@ def test_w4a16_dequant_bit_exact_identity(dev, path):
     np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("m,n,k", [(1152, 192, 128), (4096, 12288, 64)])
 @pytest.mark.parametrize("mixed", [False, True])
-def test_w4a16_dequant_bit_exact_large_tiles(dev, mixed):
-    """The large-M tile shape (m > 1024, n % 192 == 0): x repeats the
-    identity, so every output is one dequantised weight, compared bit for bit
-    on double-rounding (scale, minimum) pairs -- in every group, or mixed with
-    ordinary groups so both dequantisation paths run in one launch."""
+def test_w4a16_dequant_bit_exact_large_tiles(dev, mixed, m, n, k):
+    """The large-M tile shapes (m > 1024: 128 x 192 tiles, and 256 x 256
+    tiles once they give 768 workgroups): x repeats the identity, so every
+    output is one dequantised weight, compared bit for bit on double-rounding
+    (scale, minimum) pairs -- in every group, or mixed with ordinary groups so
+    both dequantisation paths run in one launch."""
     import qwen_image_hip.ops as ops
-    n, k, m = 192, 128, 1152
     G = k // 64
     s_adv, m_adv = _double_rounding_cases(n * G, seed=5)
     scales = s_adv.reshape(n, G).copy()
