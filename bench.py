@@ -84,24 +84,30 @@ def heavy_tailed(m, k, g):
     return t.half()
 
 
-def two_streams(run_stream, side):
-    """Run the text stream's linears on `side` and the image stream's on the
-    current stream, forked and joined with stream waits (so a captured graph
-    gets two parallel branches).  The block's two streams are independent
-    until the joint attention; the small text-stream kernels fill CUs beside
-    the image stream's.  side=None runs both on the current stream in order."""
+def two_streams(run_phase, side):
+    """Run each phase of the block (QKV, output projection, MLP) with the text
+    stream's linears on `side` and the image stream's on the current stream,
+    forked and joined with stream waits per phase (a captured graph gets two
+    parallel branches per phase).  Within a phase the two streams are
+    independent (in the model they meet at the joint attention, between the
+    phases); the small text-stream kernels fill CUs beside the image
+    stream's.  side=None runs everything on the current stream in order."""
     import torch
 
-    if side is None:
-        for stream in STREAMS:
-            run_stream(stream)
-        return
-    main = torch.cuda.current_stream()
-    side.wait_stream(main)
-    with torch.cuda.stream(side):
-        run_stream("text")
-    run_stream("image")
-    main.wait_stream(side)
+    for phase in PHASES:
+        if side is None:
+            for stream in STREAMS:
+                run_phase(stream, phase)
+            continue
+        main = torch.cuda.current_stream()
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            run_phase("text", phase)
+        run_phase("image", phase)
+        main.wait_stream(side)
+
+
+PHASES = ("qkv", "out", "mlp")
 
 
 class StepW4A4:
@@ -138,18 +144,21 @@ class StepW4A4:
         lin = self.q.linear
         f16 = torch.float16
 
-        def run_stream(stream):
+        def run_phase(stream, phase):
             b = self.bufs[stream]
             L = lambda name: self.block.layers[(stream, name)]  # noqa: E731
             w = b["work"]
-            lin(L("to_q"), w, b["x_qkv"], b["y"], out_dtype=f16)
-            lin(L("to_k"), w, b["x_qkv"], b["y"], reuse_input=True, out_dtype=f16)
-            lin(L("to_v"), w, b["x_qkv"], b["y"], reuse_input=True, out_dtype=f16)
-            lin(L("to_out"), w, b["x_out"], b["y"], out_dtype=f16)
-            lin(L("mlp_up"), w, b["x_mlp"], b["h"], out_dtype=f16, gelu=True)
-            lin(L("mlp_down"), w, b["h"], b["y"], out_dtype=f16)
+            if phase == "qkv":
+                lin(L("to_q"), w, b["x_qkv"], b["y"], out_dtype=f16)
+                lin(L("to_k"), w, b["x_qkv"], b["y"], reuse_input=True, out_dtype=f16)
+                lin(L("to_v"), w, b["x_qkv"], b["y"], reuse_input=True, out_dtype=f16)
+            elif phase == "out":
+                lin(L("to_out"), w, b["x_out"], b["y"], out_dtype=f16)
+            else:
+                lin(L("mlp_up"), w, b["x_mlp"], b["h"], out_dtype=f16, gelu=True)
+                lin(L("mlp_down"), w, b["h"], b["y"], out_dtype=f16)
 
-        two_streams(run_stream, self.side)
+        two_streams(run_phase, self.side)
 
 
 class StepW4A16:
@@ -173,17 +182,19 @@ class StepW4A16:
     def __call__(self):
         ops = self.ops
 
-        def run_stream(stream):
+        def run_phase(stream, phase):
             b = self.bufs[stream]
             L = lambda name: self.block.layers[(stream, name)]  # noqa: E731
-            for name in ("to_q", "to_k", "to_v", "to_out"):
+            names = {"qkv": ("to_q", "to_k", "to_v"), "out": ("to_out",), "mlp": ()}[phase]
+            for name in names:
                 ops.w4a16_gemm(b["x"], L(name).tiled_codes, L(name).tiled_scales, out_dtype=ops.torch.float16, y=b["y"])
-            ops.w4a16_gemm(b["x"], L("mlp_up").tiled_codes, L("mlp_up").tiled_scales, out_dtype=ops.torch.float16,
-                           gelu=True, y=b["h"])
-            ops.w4a16_gemm(b["h"], L("mlp_down").tiled_codes, L("mlp_down").tiled_scales, out_dtype=ops.torch.float16,
-                           y=b["y"])
+            if phase == "mlp":
+                ops.w4a16_gemm(b["x"], L("mlp_up").tiled_codes, L("mlp_up").tiled_scales,
+                               out_dtype=ops.torch.float16, gelu=True, y=b["h"])
+                ops.w4a16_gemm(b["h"], L("mlp_down").tiled_codes, L("mlp_down").tiled_scales,
+                               out_dtype=ops.torch.float16, y=b["y"])
 
-        two_streams(run_stream, self.side)
+        two_streams(run_phase, self.side)
 
 
 def time_fn(fn, iters, warmup):
@@ -335,8 +346,9 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="only the headline W4A4 block")
     ap.add_argument("--no-graph", action="store_true", help="time the eager step (one Python call per linear)")
-    ap.add_argument("--one-stream", action="store_true",
-                    help="run the text stream's linears after the image stream's on one HIP stream")
+    ap.add_argument("--two-streams", action="store_true",
+                    help="run each phase's text-stream linears on a second HIP stream beside the image stream's "
+                         "(measured no faster with the joins between phases)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="run only the dominant GEMM (20 launches) and a 512 MiB device copy (5 launches), "
                          "for hardware-counter runs")
@@ -355,7 +367,7 @@ def main(argv=None) -> int:
         return kernel_only()
     log("packing W4A4 block weights (fp6 operands)")
     blk4 = Block(q.SCHEME_W4A4_H256, 1)
-    step4 = StepW4A4(blk4, 2, one_stream=args.one_stream)
+    step4 = StepW4A4(blk4, 2, one_stream=not args.two_streams)
 
     # Eager: one Python call per linear.
     ms_eager = time_fn(step4, args.steps, args.warmup)
@@ -423,9 +435,7 @@ def main(argv=None) -> int:
         torch.cuda.empty_cache()
         log("packing W4A16 block weights")
         blk16 = Block(q.SCHEME_W4A16, 3)
-        # One stream: measured faster for W4A16 (the text stream's K-split
-        # workgroups, 64 KiB of LDS each, crowd the image GEMMs' CUs).
-        step16 = StepW4A16(blk16, 4, one_stream=True)
+        step16 = StepW4A16(blk16, 4, one_stream=not args.two_streams)
         ms16 = time_fn(step16, args.steps, args.warmup)
         tf16 = block_ops() / (ms16 * 1e-3) / 1e12
         extra["w4a16_block"] = {"ms_per_step": round(ms16, 4), "TFLOP_s": round(tf16, 1),
@@ -449,7 +459,7 @@ def main(argv=None) -> int:
         "dtype": "int4 x int4 exact group partials (fp6 E2M3 MFMA operands), fp32 epilogue, fp16 out", "data": "synthetic",
         "config": {"workload": "W4A4 H256 g64 one MMDiT dual-stream block linears (config 3): image M=4096 + "
                                "text M=256, hidden 3072, MLP 12288, heavy-tailed fp16 activations, online quantiser",
-                   "global_batch": 1, "seq_len": sum(STREAMS.values()), "parallelism": "single-gpu", "streams": 1 if args.one_stream else 2},
+                   "global_batch": 1, "seq_len": sum(STREAMS.values()), "parallelism": "single-gpu", "streams": 2 if args.two_streams else 1},
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
