@@ -115,7 +115,7 @@ class StepW4A4:
     distinct input quantised once (K and V reuse Q's codes), MLP up with the
     fused GELU, its fp16 output quantised again for MLP down."""
 
-    def __init__(self, block: Block, seed: int, one_stream: bool = False):
+    def __init__(self, block: Block, seed: int, one_stream: bool = True):
         import torch
         import qwen_image_hip as q
 
@@ -162,7 +162,7 @@ class StepW4A4:
 
 
 class StepW4A16:
-    def __init__(self, block: Block, seed: int, one_stream: bool = False):
+    def __init__(self, block: Block, seed: int, one_stream: bool = True):
         import torch
         from qwen_image_hip import ops
 
