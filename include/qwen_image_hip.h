@@ -39,12 +39,14 @@
 #ifndef QWEN_IMAGE_HIP_H
 #define QWEN_IMAGE_HIP_H
 
+#include <stdint.h>
+
 #ifdef __cplusplus
 extern "C" {
 #endif
 
 /* ABI version of this header; bumped on any signature change. */
-#define QI_HIP_ABI_VERSION 1
+#define QI_HIP_ABI_VERSION 2
 int qi_hip_abi_version(void);
 
 /* ---------------------------------------------------------------------------
@@ -165,6 +167,51 @@ int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *w_codes6, const float
  * be 64; clip selects the 7-candidate range-shrink search. */
 int qi_hip_pack_weights(const void *w_half, void *codes, void *scales, void *minimums, int n, int k, int scheme,
                         int clip, void *stream);
+
+/* ---- QIPACK1 container, host side ------------------------------------------
+ * Reading and checking a pack before its INT4 records are uploaded and
+ * re-laid (layout int4_pack.cplus:55-95; the loader's header and policy test
+ * transformer.cplus:342-375; the packer's verify int4_pack.cplus:733-850).
+ * These functions do host file I/O only and return the QI_PACK_* codes below
+ * (0 = success), not hipError_t. */
+#define QI_PACK_OK 0
+#define QI_PACK_EINVAL 1    /* bad argument or index */
+#define QI_PACK_EIO 2       /* open / read failed */
+#define QI_PACK_EFORMAT 3   /* not a QIPACK1 file, wrong size, unknown policy, wrong inventory */
+#define QI_PACK_ELAYOUT 4   /* record geometry, alignment, order or bounds */
+#define QI_PACK_EMETADATA 5 /* metadata checksum */
+#define QI_PACK_ETENSOR 6   /* a tensor checksum */
+#define QI_PACK_EPAYLOAD 7  /* payload checksum */
+
+typedef struct qi_pack qi_pack; /* an open pack: header, directory, file */
+typedef struct {                /* one 256-byte directory record, decoded */
+    char name[129];
+    uint32_t scheme, rank;
+    uint64_t dims[4];
+    uint32_t group_axis, group_size, scale_type, zero_type;
+    uint64_t weights_offset, weights_length, scales_offset, scales_length, zeros_offset, zeros_length;
+    uint64_t elements, tensor_checksum;
+} qi_pack_record;
+
+/* FNV-1a 64 over count bytes, continuing from hash (int4_pack.cplus:151-159). */
+uint64_t qi_fnv1a(uint64_t hash, const void *bytes, uint64_t count);
+/* Open: header (magic, size, directory placement) and directory. */
+int qi_pack_open(const char *path, qi_pack **pack);
+void qi_pack_close(qi_pack *pack);
+/* policy33 receives the 32-byte policy string plus a terminating zero. */
+int qi_pack_info(const qi_pack *pack, uint32_t *tensor_count, char *policy33, uint64_t *data_offset,
+                 uint64_t *file_bytes);
+int qi_pack_record_at(const qi_pack *pack, uint32_t index, qi_pack_record *record);
+/* Index of the record named `name`, or -1. */
+int qi_pack_find(const qi_pack *pack, const char *name);
+/* length bytes from file offset into host memory dst. */
+int qi_pack_read(const qi_pack *pack, uint64_t offset, uint64_t length, void *dst);
+/* The verify of int4_pack.cplus:733-850: policy, metadata placement and
+ * checksum, INT4 record geometry, 256-aligned monotonic tensors inside the
+ * data section ending at the file end, every tensor checksum, the payload
+ * checksum; expect_transformer != 0 also requires the full transformer
+ * inventory (297 tensors, 224 INT4 matrices). */
+int qi_pack_verify(const qi_pack *pack, int expect_transformer);
 
 #ifdef __cplusplus
 }

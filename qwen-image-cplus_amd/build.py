@@ -23,6 +23,8 @@ OUT_DIR = PKG / "qwen_image_hip"
 LIB = OUT_DIR / "libqwen_image_hip.so"
 BUILD = PKG / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+CXX = os.environ.get("CXX", "g++")
+CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-fvisibility=hidden", "-Wall", "-Wextra"]
 
 HIP_FLAGS = [
     "--offload-arch=gfx950",
@@ -61,9 +63,18 @@ def build_library(jobs: int = 8) -> Path:
         objects.append(obj)
         todo.append((src, obj))
 
+    # Host-only C++ (the QIPACK container) is compiled by the host compiler.
+    for src in sorted(CSRC.glob("*.cpp")):
+        obj = BUILD / (src.stem + ".cpp.o")
+        objects.append(obj)
+        todo.append((src, obj))
+
     def compile_one(pair):
         src, obj = pair
-        _run([HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)])
+        if src.suffix == ".cpp":
+            _run([CXX, *CXX_FLAGS, "-c", str(src), "-o", str(obj)])
+        else:
+            _run([HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)])
 
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
         list(pool.map(compile_one, todo))

@@ -332,8 +332,8 @@ QI_API int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *w_codes6, cons
     // Tile shapes (measured on MI355X): 128 x 128 with four waves when that
     // already gives two workgroups per CU; otherwise, for short M, single-
     // wave 32 x 32 tiles with an 8-deep ring, or 64 x 128 four-wave tiles
-    // when N is wide.  QI_HIP_FP6_TILES (0..4) overrides the choice, for
-    // tuning.
+    // when N is wide.  QI_HIP_FP6_TILES (0, 3 or 4) overrides the choice,
+    // for tuning.
     static const int forced = [] {
         const char *e = getenv("QI_HIP_FP6_TILES");
         return e ? atoi(e) : -1;
@@ -347,10 +347,6 @@ QI_API int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *w_codes6, cons
     switch (cfg) {
     case 0:
         return launch_fp6<2, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, s);
-    case 1:
-        return launch_fp6<1, 2, 1, 1, 8>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, s);
-    case 2:
-        return launch_fp6<2, 2, 1, 1, 8>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, s);
     case 3:
         return launch_fp6<1, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, s);
     case 4:

@@ -36,9 +36,18 @@ SIGNATURES: dict[str, list] = {
     "qi_hip_w4a4_quantize_activations_fp6": [_p, _i, _p, _p, _i, _i, _p],
     "qi_hip_relayout_w4a4_fp6": [_p, _p, _p, _p, _i, _i, _p],
     "qi_hip_w4a4_gemm_fp6": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
+    # QIPACK1 container (host I/O; QI_PACK_* status codes, not hipError_t).
+    "qi_pack_open": [ctypes.c_char_p, _p],
+    "qi_pack_info": [_p, _p, _p, _p, _p],
+    "qi_pack_record_at": [_p, ctypes.c_uint32, _p],
+    "qi_pack_find": [_p, ctypes.c_char_p],
+    "qi_pack_read": [_p, _u64, _u64, _p],
+    "qi_pack_verify": [_p, _i],
 }
+# Entry points whose return type is not int.
+RESTYPES = {"qi_fnv1a": (_u64, [_u64, _p, _u64]), "qi_pack_close": (None, [_p])}
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lib = None
 
@@ -69,6 +78,10 @@ def load() -> ctypes.CDLL:
         fn = getattr(lib, name)  # AttributeError = missing export
         fn.argtypes = args
         fn.restype = ctypes.c_int
+    for name, (restype, args) in RESTYPES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = restype
     if lib.qi_hip_abi_version() != ABI_VERSION:
         raise ImportError("libqwen_image_hip.so ABI version mismatch; rebuild it")
     _lib = lib

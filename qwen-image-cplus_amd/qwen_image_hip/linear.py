@@ -74,6 +74,20 @@ class PackedLinear:
         return cls(scheme, n, half_k * 2, tc, ts, bias, operand)
 
     @classmethod
+    def from_pack(cls, pack, name: str, device: torch.device | str = "cuda", bias: torch.Tensor | None = None,
+                  operand: str = W4A4_FP6) -> "PackedLinear":
+        """Load one INT4 record of an open ``qipack.Pack`` (the upload step of
+        transformer.cplus:386-392): its codes, scales and zeros go to the
+        device and are re-laid once; the staging copies are dropped."""
+        r = pack.record(name)
+        if r.scheme not in (SCHEME_W4A4_H256, SCHEME_W4A16) or r.group_size != ops.GROUP:
+            raise ValueError(f"{name}: scheme {r.scheme} group {r.group_size} is not an INT4 g64 record")
+        codes, scales, zeros = pack.arrays(name)
+        dev = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+        return cls.from_qipack(r.scheme, dev(codes), dev(scales).view(torch.float16),
+                               None if zeros is None else dev(zeros).view(torch.float16), bias, operand)
+
+    @classmethod
     def from_fp16(cls, scheme: int, w_half: torch.Tensor, clip: bool = False,
                   bias: torch.Tensor | None = None, operand: str = W4A4_FP6) -> "PackedLinear":
         """Quantise an fp16 [N, K] matrix with the QIPACK quantiser, then re-lay it."""

@@ -22,8 +22,12 @@ through ``PackedLinear.from_qipack``.
 """
 from __future__ import annotations
 
+import ctypes
 import struct
 from dataclasses import dataclass, field
+from pathlib import Path
+
+import numpy as np
 
 MAGIC = b"QIPACK1\x00"
 HEADER_BYTES = 256
@@ -39,12 +43,12 @@ _RECORD = struct.Struct("<128sII4QIIII QQQQQQ QQ 8s")
 assert _HEADER.size == HEADER_BYTES and _RECORD.size == RECORD_BYTES
 
 
-def fnv1a(data: bytes | memoryview, h: int = FNV_OFFSET) -> int:
-    """FNV-1a 64 (int4_pack.cplus:151-159)."""
-    mask = (1 << 64) - 1
-    for b in bytes(data):
-        h = ((h ^ b) * FNV_PRIME) & mask
-    return h
+def fnv1a(data, h: int = FNV_OFFSET) -> int:
+    """FNV-1a 64 (int4_pack.cplus:151-159), by the library's qi_fnv1a."""
+    from ._lib import load
+
+    buf = np.ascontiguousarray(np.frombuffer(memoryview(data).cast("B"), np.uint8))
+    return int(load().qi_fnv1a(h, buf.ctypes.data if buf.size else None, buf.size))
 
 
 def align_up(value: int, alignment: int = TENSOR_ALIGNMENT) -> int:
@@ -170,3 +174,155 @@ def record_checksum(blob, r: Record) -> int:
         if part is not None and len(part):
             h = fnv1a(part, h)
     return h
+
+
+# ---------------------------------------------------------------- writing --
+
+def write_pack(path, matrices, scheme: int, group: int = 64, metadata: bytes = b"",
+               model_snapshot: bytes = b"", diffusers_commit: bytes = b"") -> Header:
+    """Write a QIPACK1 file of INT4 records (the packer's layout,
+    int4_pack.cplus:476-518 and :620-720): header, directory, metadata in the
+    directory padding, then every record's codes, scales and (W4A16) zeros on
+    256-byte boundaries, with tensor, metadata and payload checksums.
+
+    ``matrices``: (name, codes uint8 [n, k/2], scales fp16 bits [n, k/g],
+    zeros fp16 bits [n, k/g] or None) in record order, host arrays.
+    """
+    records, arrays = [], []
+    for name, codes, scales, zeros in matrices:
+        n, half_k = codes.shape
+        r = int4_record(name, scheme, n, half_k * 2, group)
+        parts = [np.ascontiguousarray(codes, np.uint8), np.ascontiguousarray(scales).view(np.uint16)]
+        if scheme == SCHEME_W4A16:
+            if zeros is None:
+                raise ValueError(f"{name}: W4A16 records carry a zeros (minimums) array")
+            parts.append(np.ascontiguousarray(zeros).view(np.uint16))
+        for a, length in zip(parts, (r.weights_length, r.scales_length, r.zeros_length)):
+            if a.nbytes != length:
+                raise ValueError(f"{name}: array of {a.nbytes} bytes, record expects {length}")
+        records.append(r)
+        arrays.append(parts)
+    directory_offset = HEADER_BYTES
+    metadata_offset = directory_offset + RECORD_BYTES * len(records)
+    data_offset = align_up(metadata_offset + len(metadata))
+    file_bytes = plan(records, data_offset)
+    blob = np.zeros(file_bytes, np.uint8)
+    for r, parts in zip(records, arrays):
+        h = FNV_OFFSET
+        for a, off in zip(parts, (r.weights_offset, r.scales_offset, r.zeros_offset)):
+            raw = a.view(np.uint8).reshape(-1)
+            blob[off: off + raw.size] = raw
+            h = fnv1a(raw, h)
+        r.tensor_checksum = h
+    blob[metadata_offset: metadata_offset + len(metadata)] = np.frombuffer(metadata, np.uint8)
+    header = Header(tensor_count=len(records), directory_offset=directory_offset, data_offset=data_offset,
+                    file_bytes=file_bytes, payload_checksum=fnv1a(blob[data_offset:]),
+                    policy=policy_name(scheme, group), metadata_offset=metadata_offset,
+                    metadata_bytes=len(metadata), metadata_checksum=fnv1a(metadata),
+                    model_snapshot=model_snapshot, diffusers_commit=diffusers_commit)
+    blob[:HEADER_BYTES] = np.frombuffer(header.pack(), np.uint8)
+    for i, r in enumerate(records):
+        o = directory_offset + i * RECORD_BYTES
+        blob[o: o + RECORD_BYTES] = np.frombuffer(r.pack(), np.uint8)
+    Path(path).write_bytes(blob.tobytes())
+    return header
+
+
+# ---------------------------------------------------------------- reading --
+
+PACK_ERRORS = {1: "bad argument", 2: "I/O error", 3: "not a QIPACK1 pack of a known policy",
+               4: "record layout", 5: "metadata checksum", 6: "tensor checksum", 7: "payload checksum"}
+
+
+class QipackError(RuntimeError):
+    def __init__(self, what: str, status: int):
+        super().__init__(f"qipack: {what}: {PACK_ERRORS.get(status, status)}")
+        self.status = status
+
+
+class _CRecord(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 129), ("scheme", ctypes.c_uint32), ("rank", ctypes.c_uint32),
+                ("dims", ctypes.c_uint64 * 4), ("group_axis", ctypes.c_uint32), ("group_size", ctypes.c_uint32),
+                ("scale_type", ctypes.c_uint32), ("zero_type", ctypes.c_uint32),
+                ("weights_offset", ctypes.c_uint64), ("weights_length", ctypes.c_uint64),
+                ("scales_offset", ctypes.c_uint64), ("scales_length", ctypes.c_uint64),
+                ("zeros_offset", ctypes.c_uint64), ("zeros_length", ctypes.c_uint64),
+                ("elements", ctypes.c_uint64), ("tensor_checksum", ctypes.c_uint64)]
+
+
+class Pack:
+    """An open QIPACK1 file (qi_pack_open): header, directory, verify, and
+    each INT4 record's arrays for the upload re-layout."""
+
+    def __init__(self, path):
+        from ._lib import load
+
+        self._lib = load()
+        self._h = ctypes.c_void_p()
+        st = self._lib.qi_pack_open(str(path).encode(), ctypes.byref(self._h))
+        if st:
+            raise QipackError(f"open {path}", st)
+        count, policy = ctypes.c_uint32(), ctypes.create_string_buffer(33)
+        data_offset, file_bytes = ctypes.c_uint64(), ctypes.c_uint64()
+        self._lib.qi_pack_info(self._h, ctypes.byref(count), policy, ctypes.byref(data_offset),
+                               ctypes.byref(file_bytes))
+        self.policy = policy.value.decode()
+        self.data_offset, self.file_bytes = data_offset.value, file_bytes.value
+        self.records = []
+        for i in range(count.value):
+            c = _CRecord()
+            self._lib.qi_pack_record_at(self._h, i, ctypes.byref(c))
+            self.records.append(Record(name=c.name.decode(), scheme=c.scheme, rank=c.rank, dims=tuple(c.dims),
+                                       group_axis=c.group_axis, group_size=c.group_size, scale_type=c.scale_type,
+                                       zero_type=c.zero_type, weights_offset=c.weights_offset,
+                                       weights_length=c.weights_length, scales_offset=c.scales_offset,
+                                       scales_length=c.scales_length, zeros_offset=c.zeros_offset,
+                                       zeros_length=c.zeros_length, elements=c.elements,
+                                       tensor_checksum=c.tensor_checksum))
+        self._index = {r.name: i for i, r in enumerate(self.records)}
+
+    def close(self):
+        if self._h:
+            self._lib.qi_pack_close(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # interpreter teardown
+            pass
+
+    def verify(self, expect_transformer: bool = False) -> None:
+        """qi_pack_verify (int4_pack.cplus:733-850); raises QipackError."""
+        st = self._lib.qi_pack_verify(self._h, 1 if expect_transformer else 0)
+        if st:
+            raise QipackError("verify", st)
+
+    def read(self, offset: int, length: int) -> np.ndarray:
+        out = np.empty(length, np.uint8)
+        st = self._lib.qi_pack_read(self._h, offset, length, out.ctypes.data if length else None)
+        if st:
+            raise QipackError(f"read {length} bytes at {offset}", st)
+        return out
+
+    def record(self, name: str) -> Record:
+        if name not in self._index:
+            raise KeyError(f"no record {name!r} in the pack")
+        return self.records[self._index[name]]
+
+    def arrays(self, name: str):
+        """(codes uint8 [n, k/2], scales fp16 bits [n, G], zeros or None) of an INT4 record."""
+        r = self.record(name)
+        n, k = r.dims[0], r.dims[1]
+        g = k // r.group_size
+        codes = self.read(r.weights_offset, r.weights_length).reshape(n, k // 2)
+        scales = self.read(r.scales_offset, r.scales_length).view(np.uint16).reshape(n, g)
+        zeros = (self.read(r.zeros_offset, r.zeros_length).view(np.uint16).reshape(n, g)
+                 if r.zeros_length else None)
+        return codes, scales, zeros

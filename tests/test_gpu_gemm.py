@@ -301,3 +301,33 @@ def test_w4a16_dequant_bit_exact_large_tiles(dev, mixed, m, n, k):
     tc, ts = ops.relayout_w4a16(_dev(codes, dev), _h(scales, dev), _h(mins, dev))
     got = ops.w4a16_gemm(_dev(x, dev), tc, ts).cpu().numpy()                                  # [m, n]
     np.testing.assert_array_equal(got.view(np.uint32), np.tile(want.T, (m // k, 1)).view(np.uint32))
+
+
+# ------------------------------------------------------- QIPACK file upload --
+
+@pytest.mark.parametrize("scheme", [5, 6])
+def test_linear_from_qipack_file(dev, tmp_path, scheme):
+    """Quantise on the device, write a QIPACK1 file, verify it, load the
+    record back through the upload re-layout: the linear's output equals the
+    in-memory record's bit for bit (the arrays round-trip exactly)."""
+    import qwen_image_hip as q
+    from qwen_image_hip import qipack
+    import qwen_image_hip.ops as ops
+    n, k, rows = 256, 512, 96
+    w = weights_f16(n, k, 950 + scheme)
+    codes, scales, mins = ops.pack_weights(_h(w, dev), scheme, clip=scheme == 6)
+    host = lambda t: None if t is None else t.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)  # noqa
+    path = tmp_path / "w.qipack"
+    qipack.write_pack(path, [("transformer_blocks.0.img_mlp.net.0.proj.weight", codes.cpu().numpy(),
+                              host(scales), host(mins))], scheme)
+    direct = q.PackedLinear.from_qipack(scheme, codes, scales, mins)
+    with qipack.Pack(path) as p:
+        p.verify()
+        loaded = q.PackedLinear.from_pack(p, "transformer_blocks.0.img_mlp.net.0.proj.weight", dev)
+    x = _dev(heavy_tailed(rows, k, 951), dev)
+    if scheme == 5:
+        x = x.half()
+    work = q.Work(rows_max=rows, k_max=k, device=dev)
+    a = q.linear(direct, work, x).cpu().numpy()
+    b = q.linear(loaded, work, x).cpu().numpy()
+    np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))

@@ -54,3 +54,85 @@ def test_record_checksum_order():
     w, s, z = qipack.tensor_arrays(blob, r)
     want = qipack.fnv1a(bytes(z), qipack.fnv1a(bytes(s), qipack.fnv1a(bytes(w))))
     assert qipack.record_checksum(blob, r) == want
+
+
+# ------------------------------------------------- container write / verify --
+
+import pytest  # noqa: E402
+
+
+def _pack_file(tmp_path, scheme=5, shapes=((64, 256), (32, 512)), metadata=b'{"source": "synthetic"}'):
+    g = np.random.default_rng(7)
+    mats = []
+    for i, (n, k) in enumerate(shapes):
+        codes = g.integers(0, 256, (n, k // 2), dtype=np.uint8)
+        scales = (g.random((n, k // 64)) * 0.01 + 0.001).astype(np.float16).view(np.uint16)
+        zeros = (-(g.random((n, k // 64)) * 0.05)).astype(np.float16).view(np.uint16) if scheme == 5 else None
+        mats.append((f"transformer_blocks.{i}.attn.to_q.weight", codes, scales, zeros))
+    path = tmp_path / "model.qipack"
+    qipack.write_pack(path, mats, scheme, metadata=metadata)
+    return path, mats
+
+
+@pytest.mark.parametrize("scheme", [5, 6])
+def test_write_open_verify_round_trip(tmp_path, scheme):
+    path, mats = _pack_file(tmp_path, scheme)
+    with qipack.Pack(path) as p:
+        p.verify()
+        assert p.policy == qipack.policy_name(scheme)
+        assert [r.name for r in p.records] == [m[0] for m in mats]
+        for name, codes, scales, zeros in mats:
+            c, s, z = p.arrays(name)
+            np.testing.assert_array_equal(c, codes)
+            np.testing.assert_array_equal(s, scales)
+            if scheme == 5:
+                np.testing.assert_array_equal(z, zeros)
+            else:
+                assert z is None
+            r = p.record(name)
+            assert r.weights_offset % 256 == 0 and r.scales_offset % 256 == 0
+            assert r.tensor_checksum == oracle.fnv1a(zeros.tobytes() if zeros is not None else b"",
+                                                     oracle.fnv1a(scales.tobytes(), oracle.fnv1a(codes.tobytes())))
+        with pytest.raises(qipack.QipackError, match="not a QIPACK1"):
+            p.verify(expect_transformer=True)  # 2 records, not the 297-tensor transformer
+
+
+def _corrupt(path, offset, value=None):
+    b = bytearray(path.read_bytes())
+    b[offset] = (b[offset] ^ 0x5A) if value is None else value
+    path.write_bytes(bytes(b))
+
+
+def test_verify_catches_each_kind_of_damage(tmp_path):
+    path, mats = _pack_file(tmp_path)
+    with qipack.Pack(path) as p:
+        r0, meta_off, data_off = p.records[0], 256 + 256 * len(mats), p.data_offset
+    cases = {
+        "tensor checksum": r0.scales_offset + 3,        # a scale byte
+        "metadata checksum": meta_off + 2,              # a metadata byte
+        "payload checksum": 48,                         # the header's payload checksum field
+    }
+    for what, off in cases.items():
+        bad = tmp_path / f"bad_{off}.qipack"
+        bad.write_bytes(path.read_bytes())
+        _corrupt(bad, off)
+        with qipack.Pack(bad) as p, pytest.raises(qipack.QipackError, match=what):
+            p.verify()
+    # a record's weights moved off its 256-byte boundary
+    bad = tmp_path / "misaligned.qipack"
+    bad.write_bytes(path.read_bytes())
+    _corrupt(bad, 256 + 184, (r0.weights_offset + 16) & 0xFF)
+    with qipack.Pack(bad) as p, pytest.raises(qipack.QipackError, match="record layout"):
+        p.verify()
+    # not a pack, and a truncated one
+    bad = tmp_path / "magic.qipack"
+    bad.write_bytes(path.read_bytes())
+    _corrupt(bad, 0, ord("X"))
+    with pytest.raises(qipack.QipackError, match="not a QIPACK1"):
+        qipack.Pack(bad)
+    bad = tmp_path / "short.qipack"
+    bad.write_bytes(path.read_bytes()[:-256])
+    with pytest.raises(qipack.QipackError, match="not a QIPACK1"):
+        qipack.Pack(bad)
+    with pytest.raises(qipack.QipackError, match="I/O"):
+        qipack.Pack(tmp_path / "absent.qipack")
