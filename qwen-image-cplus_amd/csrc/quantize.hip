@@ -55,6 +55,16 @@ __device__ __forceinline__ void load4<uint16_t>(const uint16_t *src, float v[4])
     v[3] = h2f(static_cast<uint16_t>(t.y >> 16));
 }
 
+// v from another lane of the same 16-lane row, by a DPP control word.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+
 // LDS word of element i of a chunk: an XOR swizzle that makes every access
 // pattern below (4 consecutive words per lane, and the strided butterfly
 // quadruples of strides 4, 16, 64) conflict-free for 32 lanes at a time.
@@ -109,8 +119,13 @@ __device__ __forceinline__ void quantize_chunk(float (&v)[4], float *buf, int la
     // halving, else 1; exact).  absmax is order-free.
     constexpr float unit = HALF ? 1.0f : 16.0f;
     float peak = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-#pragma unroll
-    for (int s = 8; s > 0; s >>= 1) peak = fmaxf(peak, __shfl_xor(peak, s, 64));
+    // Max over the 16 lanes of the group with DPP moves (no LDS round
+    // trips): lane ^ 1, lane ^ 2 within quads, then the 8-lane and 16-lane
+    // mirrors pair the quads and the two halves.
+    peak = fmaxf(peak, dpp_f32<0xB1>(peak));   // quad_perm [1,0,3,2]
+    peak = fmaxf(peak, dpp_f32<0x4E>(peak));   // quad_perm [2,3,0,1]
+    peak = fmaxf(peak, dpp_f32<0x141>(peak));  // row_half_mirror
+    peak = fmaxf(peak, dpp_f32<0x140>(peak));  // row_mirror
     // gemm.cu:45-48: IEEE division by 7, fp16 RNE scale, IEEE v / scale,
     // rint (nearest even), clamp to [-7, 7].
     scale_bits = f2h(fmaxf((peak * (1.0f / unit)) / 7.0f, 5.9604645e-08f));
@@ -222,7 +237,7 @@ __global__ __launch_bounds__(32 / RPW * WAVE) void quantize_fp6_strip_kernel(
         const int r32 = wave * RPW + i;
         const uint32_t bits =
             e2m3_of(q[0]) | (e2m3_of(q[1]) << 6) | (e2m3_of(q[2]) << 12) | (e2m3_of(q[3]) << 18);
-        const uint32_t next = static_cast<uint32_t>(__shfl_down(static_cast<int>(bits), 1, 64));
+        const uint32_t next = dpp_u32<0x101>(bits);  // row_shl:1 -- lane + 1 (unused by p = 3)
         const int slot = (sl >> 1) * 32 + r32;
         uint32_t *dst = blocks + (gb * FP6_BLOCK + ((sl & 1) ? FP6_HALF0 + slot * 12 : slot * 16)) / 4;
         if (p < 3)
@@ -272,10 +287,10 @@ static int launch_quantize(const In *x, void *codes, void *scales, int m, int k,
     if (FMT == 1) {
         if (chunks > 65535) return kInvalid;
         const dim3 grid(static_cast<unsigned>((m + 31) / 32), static_cast<unsigned>(chunks));
-        // Eight rows per wave when there are rows enough to fill the chip,
-        // else two (16 waves per workgroup).
+        // Four rows per wave (8 waves per workgroup) when there are rows
+        // enough to fill the chip, else two (16 waves).
         if (m >= 1024)
-            quantize_fp6_strip_kernel<In, 8><<<grid, dim3(4 * WAVE), 0, stream>>>(
+            quantize_fp6_strip_kernel<In, 4><<<grid, dim3(8 * WAVE), 0, stream>>>(
                 x, static_cast<uint8_t *>(codes), static_cast<uint16_t *>(scales), m, k);
         else
             quantize_fp6_strip_kernel<In, 2><<<grid, dim3(16 * WAVE), 0, stream>>>(
