@@ -64,31 +64,41 @@ __device__ __forceinline__ v8i fp6_operand(v4i lo, v4i hi) {
 }
 
 template <int TM, int TN, int WM, int WN, int NSTAGE>
-__global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2))) void w4a4_fp6_kernel(
-    const uint8_t *__restrict__ a6, const uint8_t *__restrict__ w6, const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi,
-    int m, int n, int k) {
+struct Fp6Shape {
+    static constexpr int MT = WM * TM, NTL = WN * TN;  // 32-row tiles of the block
+    static constexpr int BM = MT * 32, BN = NTL * 32;
+    static constexpr int TILE = 2048, SLOT = (MT + NTL) * TILE;
+    static constexpr int LDS_BYTES = NSTAGE * SLOT;
+};
+
+// The GEMM work of one workgroup: `count` output tiles of BM x BN, the j-th
+// starting at 32-row tile coordinates map(j, mt0, nt0).  The LDS ring and
+// the software pipeline run on across tile boundaries: the loads of the next
+// tile's first groups are in flight while the current tile finishes, and its
+// first partial tiles are formed during the current tile's last fp32 step,
+// so only the epilogue stores sit between two tiles.
+template <int TM, int TN, int WM, int WN, int NSTAGE, bool WHOLE, typename Map>
+__device__ __forceinline__ void fp6_tiles(uint8_t *lds, const uint8_t *__restrict__ a6,
+                                          const uint8_t *__restrict__ w6, const float *__restrict__ bias,
+                                          void *__restrict__ y, int out_type, int epi, int m, int n, int k, int count,
+                                          Map map) {
+    using S = Fp6Shape<TM, TN, WM, WN, NSTAGE>;
     constexpr int NW = WM * WN;
-    constexpr int MT = WM * TM, NTL = WN * TN;  // 32-row tiles of the block
-    constexpr int BM = MT * 32, BN = NTL * 32;
-    constexpr int HALVES = 2 * (MT + NTL);      // 768-byte loads per group
+    constexpr int MT = S::MT, NTL = S::NTL;
+    constexpr int HALVES = 2 * (MT + NTL);  // 1 KiB loads per group
     static_assert(HALVES % NW == 0, "loader mapping");
     constexpr int L_PER_W = HALVES / NW;
     static_assert(TN <= 2, "scale products pair the n-tiles");
     constexpr int LOADS_PER_GROUP = L_PER_W;  // per wave
-    constexpr int TILE = 2048, SLOT = (MT + NTL) * TILE;
+    constexpr int TILE = S::TILE, SLOT = S::SLOT;
     constexpr uint32_t BLOCK = FP6_BLOCK;  // global bytes per (tile, group)
-    static_assert(NSTAGE * SLOT <= 160 * 1024, "LDS size");
-    __shared__ __attribute__((aligned(16))) uint8_t lds[NSTAGE * SLOT];
+    static_assert(S::LDS_BYTES <= 160 * 1024, "LDS size");
 
     const int groups = k >> 6;
     const int lane = threadIdx.x & (WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WN, wn = wave % WN;
     const int r32 = lane & 31;
-    const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
-    int tm, tn;
-    tile_of_block(blockIdx.x, tiles_m, tiles_n, 8, tm, tn);
-    const int mt0 = tm * MT, nt0 = tn * NTL;  // first 32-row tiles
     const int m_tiles = (m + 31) / 32, n_tiles = n / 32;
 
     const uint32_t a_bytes = static_cast<uint32_t>(m_tiles) * groups * BLOCK;
@@ -97,18 +107,38 @@ __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2)
     const v4i_rsrc rw = raw_rsrc(w6, w_bytes);
 
     // This wave's operand loads: half blocks H0 .. H0 + L_PER_W - 1 of the
-    // block's (MT + NTL) tiles, activation tiles first.  Missing tiles read
-    // past the buffer end, which returns zeros.
+    // block's (MT + NTL) tiles, activation tiles first, for output tile j.
+    // With WHOLE (every tile of every output tile exists: count > 1 is only
+    // used so) the lane part of each address is fixed and the tile part is
+    // a scalar offset, so a tile switch only changes scalar registers; tiles
+    // j >= count repeat the last tile's loads, which are never consumed.
+    // Otherwise (one output tile) missing tiles read past the buffer end,
+    // which returns zeros.
     const int H0 = wave * L_PER_W;
     uint32_t vo[L_PER_W];
+    uint32_t sbase[L_PER_W];
+    auto set_tile_loads = [&](int j) {
+        if (WHOLE && j >= count) return;
+        int mt0 = m_tiles, nt0 = n_tiles;
+        if (j < count) map(j, mt0, nt0);
 #pragma unroll
-    for (int u = 0; u < L_PER_W; ++u) {
-        const int H = H0 + u, X = H >> 1, half = H & 1;
-        const bool from_a = H < 2 * MT;
-        const int t = from_a ? mt0 + X : nt0 + X - MT;
-        const bool ok = from_a ? t < m_tiles : t < n_tiles;
-        vo[u] = ok ? static_cast<uint32_t>(t) * groups * BLOCK + (half ? 1024u + lane * 12u : lane * 16u)
-                   : (from_a ? a_bytes : w_bytes);
+        for (int u = 0; u < L_PER_W; ++u) {
+            const int H = H0 + u, X = H >> 1, half = H & 1;
+            const bool from_a = H < 2 * MT;
+            const int t = from_a ? mt0 + X : nt0 + X - MT;
+            if constexpr (WHOLE) {
+                sbase[u] = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(t) * groups * BLOCK);
+            } else {
+                const bool ok = from_a ? t < m_tiles : t < n_tiles;
+                vo[u] = ok ? static_cast<uint32_t>(t) * groups * BLOCK + (half ? 1024u + lane * 12u : lane * 16u)
+                           : (from_a ? a_bytes : w_bytes);
+                sbase[u] = 0;
+            }
+        }
+    };
+    if constexpr (WHOLE) {
+#pragma unroll
+        for (int u = 0; u < L_PER_W; ++u) vo[u] = ((H0 + u) & 1) ? 1024u + lane * 12u : lane * 16u;
     }
 
     // Every vector-memory load of the loop is a direct-to-LDS load whose
@@ -122,17 +152,19 @@ __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2)
         for (int u = 0; u < L_PER_W; ++u) {
             const int H = H0 + u;
             dma_dwordx4(H < 2 * MT ? ra : rw, lds0 + slot * SLOT + (H >> 1) * TILE + (H & 1) * 1024, vo[u],
-                        g * BLOCK);
+                        sbase[u] + g * BLOCK);
         }
     };
 
     v16f acc[TN][TM];
+    auto zero_acc = [&]() {
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
+                for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
+    };
 
     // This lane's fragments: weight tile j half h at
     // lds[slot][MT + wn * TN + j][h][16 lane], activation tile i likewise.
@@ -193,110 +225,246 @@ __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2)
         for (int r = 0; r < 16; ++r) acc[j][i][r] = __builtin_fmaf(p[j][i][r], sp[i][16 * j + r], acc[j][i][r]);
     };
 
+    // acc[j][i][4a + r] = y[row, col]: row = m-tile i, lane % 32; col = n-tile
+    // j, 8a + 4 * (lane / 32) + r.
+    auto store_tile = [&](int jt) {
+        int mt0, nt0;
+        map(jt, mt0, nt0);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int row = (mt0 + wm * TM + i) * 32 + r32;
+            if (row >= m) continue;
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int tile_col = (nt0 + wn * TN + j) * 32;
+                if (tile_col >= n) continue;
+#pragma unroll
+                for (int a = 0; a < 4; ++a) {
+                    const int col = tile_col + 8 * a + 4 * (lane >> 5);
+                    float v[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) v[r] = epilogue(acc[j][i][4 * a + r], bias, col + r, epi);
+                    const size_t idx = static_cast<size_t>(row) * n + col;
+                    if (out_type == QI_HIP_OUT_F16) {
+                        uint2 h;
+                        h.x = static_cast<uint32_t>(f2h(v[0])) | (static_cast<uint32_t>(f2h(v[1])) << 16);
+                        h.y = static_cast<uint32_t>(f2h(v[2])) | (static_cast<uint32_t>(f2h(v[3])) << 16);
+                        *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(y) + idx) = h;
+                    } else {
+                        *reinterpret_cast<float4 *>(reinterpret_cast<float *>(y) + idx) =
+                            float4{v[0], v[1], v[2], v[3]};
+                    }
+                }
+            }
+        }
+    };
+
     // Software pipeline.  The matrix-core work of group g + 1 runs during
     // the fp32 step of group g, interleaved tile by tile: the fp32 step of
     // tile (j, i) frees p[j][i], whose next partial tile is issued at once and
     // computes while the vector unit steps the next tile; sp[i] is refilled
     // once both n-tiles of row tile i have used it.  So the fragments are
-    // needed one group ahead only.  Per group g (slots are g mod NSTAGE):
-    //   wait until this wave's loads of g + 1 are done, barrier (then every
-    //   wave's are, and every wave has consumed its reads of slot g);
-    //   issue the loads of g + NSTAGE into slot g;
-    //   read the fragments of g + 1;
-    //   fp32 step of g interleaved with the matrix-core work of g + 1.
-    // Loads past the last group read harmless bytes into slots that are
-    // never consumed, keeping the loads per group constant; the last step's
+    // needed one group ahead only.  Groups are numbered along the whole
+    // sequence (tile j's group g is j * groups + g).  Per group (slots are
+    // the group's number mod NSTAGE):
+    //   wait until this wave's loads of the next group are done, barrier
+    //   (then every wave's are, and every wave has consumed its reads of
+    //   this group's slot);
+    //   issue the loads of the group NSTAGE ahead into this slot;
+    //   read the fragments of the next group;
+    //   fp32 step of this group interleaved with the next one's matrix-core
+    //   work.
+    // Loads past the last group read zeros into slots that are never
+    // consumed, keeping the loads per group constant; the last step's
     // matrix-core work is likewise discarded.
     static_assert(NSTAGE % 4 == 0, "whole quarters of the ring per group count (groups % 4 == 0)");
     static_assert(NSTAGE >= 2 && (NSTAGE - 1) * LOADS_PER_GROUP <= 63, "vmcnt range");
+    // Several tiles (WHOLE) use a 4-deep ring, so that tiles end on ring
+    // boundaries; otherwise count == 1.
     Frags F;
+    // One step of the ring: the fp32 step of the group in slot u, the loads
+    // of group `gload` (of the tile set_tile_loads chose) into slot u, and
+    // the next group's matrix-core work -- except in the last step of a tile
+    // (LAST), which leaves that work until the tile is stored, so that the
+    // partials are not live across the epilogue.
+    auto group_step = [&](auto uc, int gload, auto last_c) {
+        constexpr int u = decltype(uc)::value;
+        constexpr bool LAST = decltype(last_c)::value;
+        // Scheduling fences pin the order; without them the compiler
+        // gathers the matrix-core work into one block.  A bare s_barrier:
+        // __syncthreads' release fence would also wait for the loads of the
+        // groups still in flight.
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((NSTAGE - 2) * LOADS_PER_GROUP) : "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        issue(gload, u);
+        if constexpr (!LAST) read_frags(std::integral_constant<int, (u + 1) % NSTAGE>{}, F);
+        __builtin_amdgcn_sched_barrier(0);
+        // Tile q = i * TN + j.  Its next partial tile is issued LAG tiles
+        // later, so the fragment reads above have the fp32 steps of LAG
+        // tiles to land.
+        constexpr int T = TM * TN, LAG = T > 2 ? 2 : 0;
+        static_for<T + LAG>([&](auto qc) {
+            constexpr int q = decltype(qc)::value;
+            if constexpr (q < T) {
+                constexpr int i = q / TN, j = q % TN;
+                tile_fma(j, i);
+                __builtin_amdgcn_sched_barrier(0);
+                // sp[i] is free once the last tile of row tile i has
+                // stepped.
+                if constexpr (j == TN - 1 && !LAST) {
+                    scale_mfma(F, i);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            if constexpr (q >= LAG && !LAST) {
+                constexpr int d = q - LAG;
+                tile_mfma(F, d % TN, d / TN);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        });
+    };
+
+    // The matrix-core work of the group whose fragments F holds.
+    auto start_group = [&]() {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            scale_mfma(F, i);
+#pragma unroll
+            for (int j = 0; j < TN; ++j) tile_mfma(F, j, i);
+        }
+    };
+    using Mid = std::false_type;
+    using Last = std::true_type;
+
+    zero_acc();
+    set_tile_loads(0);
 #pragma unroll
     for (int q = 0; q < NSTAGE; ++q) issue(q, q);
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTAGE - 1) * LOADS_PER_GROUP) : "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     read_frags(std::integral_constant<int, 0>{}, F);
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-        scale_mfma(F, i);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) tile_mfma(F, j, i);
-    }
-    for (int g0 = 0; g0 < groups; g0 += NSTAGE) {
-        static_for<NSTAGE>([&](auto uc) {
-            constexpr int u = decltype(uc)::value;
-            const int g = g0 + u;
-            // groups is a multiple of 4, so only whole quarters of a
-            // NSTAGE = 8 ring can be missing at the end; the test is uniform
-            // and covers a whole iteration, so no partial tile stays live
-            // across iterations.
-            if (u < 4 || g < groups) {
-                // Scheduling fences pin the order; without them the compiler
-                // gathers the matrix-core work into one block.  A bare
-                // s_barrier: __syncthreads' release fence would also wait for
-                // the loads of the groups still in flight.
-                __builtin_amdgcn_sched_barrier(0);
-                asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((NSTAGE - 2) * LOADS_PER_GROUP) : "memory");
-                __builtin_amdgcn_s_barrier();
-                asm volatile("" ::: "memory");
-                issue(g + NSTAGE, u);
-                read_frags(std::integral_constant<int, (u + 1) % NSTAGE>{}, F);
-                __builtin_amdgcn_sched_barrier(0);
-                // Tile q = i * TN + j.  Its next partial tile is issued LAG
-                // tiles later, so the fragment reads above have the fp32
-                // steps of LAG tiles to land.
-                constexpr int T = TM * TN, LAG = T > 2 ? 2 : 0;
-                static_for<T + LAG>([&](auto qc) {
-                    constexpr int q = decltype(qc)::value;
-                    if constexpr (q < T) {
-                        constexpr int i = q / TN, j = q % TN;
-                        tile_fma(j, i);
-                        __builtin_amdgcn_sched_barrier(0);
-                        // sp[i] is free once the last tile of row tile i has
-                        // stepped.
-                        if constexpr (j == TN - 1) {
-                            scale_mfma(F, i);
-                            __builtin_amdgcn_sched_barrier(0);
-                        }
-                    }
-                    if constexpr (q >= LAG) {
-                        constexpr int d = q - LAG;
-                        tile_mfma(F, d % TN, d / TN);
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
-                });
-            }
-        });
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-
-    // acc[j][i][4a + r] = y[row, col]: row = m-tile i, lane % 32; col = n-tile
-    // j, 8a + 4 * (lane / 32) + r.
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-        const int row = (mt0 + wm * TM + i) * 32 + r32;
-        if (row >= m) continue;
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int tile_col = (nt0 + wn * TN + j) * 32;
-            if (tile_col >= n) continue;
-#pragma unroll
-            for (int a = 0; a < 4; ++a) {
-                const int col = tile_col + 8 * a + 4 * (lane >> 5);
-                float v[4];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) v[r] = epilogue(acc[j][i][4 * a + r], bias, col + r, epi);
-                const size_t idx = static_cast<size_t>(row) * n + col;
-                if (out_type == QI_HIP_OUT_F16) {
-                    uint2 h;
-                    h.x = static_cast<uint32_t>(f2h(v[0])) | (static_cast<uint32_t>(f2h(v[1])) << 16);
-                    h.y = static_cast<uint32_t>(f2h(v[2])) | (static_cast<uint32_t>(f2h(v[3])) << 16);
-                    *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(y) + idx) = h;
-                } else {
-                    *reinterpret_cast<float4 *>(reinterpret_cast<float *>(y) + idx) = float4{v[0], v[1], v[2], v[3]};
-                }
+    start_group();
+    if constexpr (WHOLE) {
+        static_assert(NSTAGE == 4, "tiles end on ring boundaries");
+        // Tiles end on ring boundaries (groups % 4 == 0).  One loop over the
+        // rings of all the tiles; at a tile's end (a uniform branch) the
+        // load offsets move to the next tile and the tile is stored.
+        const int total = count * groups;
+        int gl = NSTAGE, jl = 0, gc = 0, jc = 0;  // next loads: tile jl group gl; step: tile jc group gc
+        if (gl >= groups) {
+            gl -= groups;
+            jl = 1;
+            set_tile_loads(1);
+        }
+        for (int g0 = 0; g0 < total; g0 += NSTAGE) {
+            static_for<NSTAGE>([&](auto uc) { group_step(uc, gl + decltype(uc)::value, Mid{}); });
+            // Branch-free: the load tile is re-derived every ring.
+            gl += NSTAGE;
+            const bool wrap = gl >= groups;
+            gl = wrap ? gl - groups : gl;
+            jl += wrap ? 1 : 0;
+            set_tile_loads(min(jl, count - 1));
+            gc += NSTAGE;
+            if (gc >= groups) {
+                gc = 0;
+                store_tile(jc);
+                zero_acc();
+                ++jc;
             }
         }
+    } else {
+        // One tile (count == 1).  groups is a multiple of 4, so only whole
+        // quarters of a NSTAGE = 8 ring can be missing at the end; the test
+        // is uniform and covers a whole ring, so no partial tile stays live
+        // across rings.  Loads past the last group read bytes that are never
+        // consumed.
+        for (int g0 = 0; g0 < groups; g0 += NSTAGE)
+            static_for<NSTAGE>([&](auto uc) {
+                constexpr int u = decltype(uc)::value;
+                if (u < 4 || g0 + u < groups) group_step(uc, g0 + NSTAGE + u, Mid{});
+            });
+        store_tile(0);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// One output tile per workgroup, in XCD-aware order.
+template <int TM, int TN, int WM, int WN, int NSTAGE>
+__global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2))) void w4a4_fp6_kernel(
+    const uint8_t *__restrict__ a6, const uint8_t *__restrict__ w6, const float *__restrict__ bias,
+    void *__restrict__ y, int out_type, int epi, int m, int n, int k) {
+    using S = Fp6Shape<TM, TN, WM, WN, NSTAGE>;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[S::LDS_BYTES];
+    const int tiles_m = (m + S::BM - 1) / S::BM, tiles_n = (n + S::BN - 1) / S::BN;
+    int tm, tn;
+    tile_of_block(blockIdx.x, tiles_m, tiles_n, 8, tm, tn);
+    fp6_tiles<TM, TN, WM, WN, NSTAGE, false>(lds, a6, w6, bias, y, out_type, epi, m, n, k, 1,
+                                      [&](int, int &mt0, int &nt0) {
+                                          mt0 = tm * S::MT;
+                                          nt0 = tn * S::NTL;
+                                      });
+}
+
+// Persistent form for large problems: gridDim.x workgroups (two per CU)
+// walk the 128 x 128 tiles t = blockIdx.x + j * gridDim.x, t < full_tiles,
+// in XCD-aware order, with one pipeline across their tiles.  When the
+// tiles left after the full rounds would keep at most half of the
+// workgroups busy, the host passes them as half_units = 2 x that many
+// 64 x 128 halves instead (one per workgroup), so that the last round is as
+// long as half a full one with every workgroup busy.  Halves of one tile go
+// to workgroups on the same XCD (ids 8 apart) when the count allows.  A
+// workgroup's tile list (at most FP6_MAX_TILES tiles, checked by the host)
+// is computed once into LDS, outside the pipelined loop.
+constexpr int FP6_MAX_TILES = 128;
+
+template <int TN, int WM, int WN, int NSTAGE>
+__global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2))) void w4a4_fp6_persistent_kernel(
+    const uint8_t *__restrict__ a6, const uint8_t *__restrict__ w6, const float *__restrict__ bias,
+    void *__restrict__ y, int out_type, int epi, int m, int n, int k, int full_tiles, int half_units) {
+    static_assert(NSTAGE == 4, "tiles end on ring boundaries");
+    using S2 = Fp6Shape<2, TN, WM, WN, NSTAGE>;
+    using S1 = Fp6Shape<1, TN, WM, WN, NSTAGE>;
+    static_assert(S2::LDS_BYTES >= S1::LDS_BYTES, "one LDS ring for both phases");
+    __shared__ __attribute__((aligned(16))) uint8_t lds[S2::LDS_BYTES];
+    __shared__ uint32_t tile_list[FP6_MAX_TILES];  // mt0 | nt0 << 16
+    const int tiles_m = (m + S2::BM - 1) / S2::BM, tiles_n = (n + S2::BN - 1) / S2::BN;
+    const int b = blockIdx.x, stride = gridDim.x;
+    const int count = b < full_tiles ? (full_tiles - 1 - b) / stride + 1 : 0;
+    for (int j = threadIdx.x; j < count; j += blockDim.x) {
+        int tm, tn;
+        tile_of_block(b + j * stride, tiles_m, tiles_n, 8, tm, tn);
+        tile_list[j] = static_cast<uint32_t>(tm * S2::MT) | (static_cast<uint32_t>(tn * S2::NTL) << 16);
+    }
+    __syncthreads();
+    if (count > 0)
+        fp6_tiles<2, TN, WM, WN, NSTAGE, true>(lds, a6, w6, bias, y, out_type, epi, m, n, k, count,
+                                         [&](int j, int &mt0, int &nt0) {
+                                             const uint32_t e = __builtin_amdgcn_readfirstlane(tile_list[j]);
+                                             mt0 = static_cast<int>(e & 0xFFFFu);
+                                             nt0 = static_cast<int>(e >> 16);
+                                         });
+    if (b < half_units) {
+        // The ring is reused: every wave has finished with it (each wave's
+        // own loads were drained at the end of the first phase).
+        __syncthreads();
+        int t, half;
+        if (half_units % 16 == 0) {
+            t = full_tiles + (b >> 4) * 8 + (b & 7);
+            half = (b >> 3) & 1;
+        } else {
+            t = full_tiles + (b >> 1);
+            half = b & 1;
+        }
+        int tm, tn;
+        tile_of_block(t, tiles_m, tiles_n, 8, tm, tn);
+        fp6_tiles<1, TN, WM, WN, NSTAGE, false>(lds, a6, w6, bias, y, out_type, epi, m, n, k, 1,
+                                         [&](int, int &mt0, int &nt0) {
+                                             mt0 = tm * S2::MT + half * S1::MT;
+                                             nt0 = tn * S1::NTL;
+                                         });
     }
 }
 
@@ -308,6 +476,46 @@ static int launch_fp6(const void *a6, const void *w6, const float *bias, void *y
     if (blocks > 0x7FFFFFFFLL) return kInvalid;
     w4a4_fp6_kernel<TM, TN, WM, WN, NSTAGE><<<dim3(static_cast<unsigned>(blocks)), dim3(WM * WN * WAVE), 0, stream>>>(
         static_cast<const uint8_t *>(a6), static_cast<const uint8_t *>(w6), bias, y, out_type, epi, m, n, k);
+    return launch_status();
+}
+
+// Compute units of the current device, read once per device.
+static int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int c = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+        cus[dev] = c;
+    }
+    return cus[dev];
+}
+
+// 128 x 128 tiles, two workgroups per CU, persistent (see the kernel).
+static int launch_fp6_persistent(const void *a6, const void *w6, const float *bias, void *y, int out_type, int epi,
+                                 int m, int n, int k, hipStream_t stream) {
+    const long long tiles = static_cast<long long>((m + 127) / 128) * ((n + 127) / 128);
+    const long long slots = 2LL * device_cus();
+    long long full = tiles, halves = 0, grid;
+    if (tiles >= slots) {
+        const long long rem = tiles % slots;
+        if (rem > 0 && 2 * rem <= slots) {
+            full = tiles - rem;
+            halves = 2 * rem;
+        }
+        grid = slots;
+    } else if (2 * tiles <= slots) {
+        full = 0;
+        halves = 2 * tiles;
+        grid = halves;
+    } else {
+        grid = tiles;
+    }
+    if (tiles > 0x7FFFFFFFLL || (full + grid - 1) / grid > FP6_MAX_TILES) return kInvalid;
+    w4a4_fp6_persistent_kernel<2, 2, 2, 4><<<dim3(static_cast<unsigned>(grid)), dim3(4 * WAVE), 0, stream>>>(
+        static_cast<const uint8_t *>(a6), static_cast<const uint8_t *>(w6), bias, y, out_type, epi, m, n, k,
+        static_cast<int>(full), static_cast<int>(halves));
     return launch_status();
 }
 
@@ -330,10 +538,11 @@ QI_API int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *w_codes6, cons
         return kInvalid;
     hipStream_t s = stream_of(stream);
     // Tile shapes (measured on MI355X): 128 x 128 with four waves when that
-    // already gives two workgroups per CU; otherwise, for short M, single-
+    // already gives two workgroups per CU (persistent when M and N are
+    // multiples of 128); otherwise, for short M, single-
     // wave 32 x 32 tiles with an 8-deep ring, or 64 x 128 four-wave tiles
-    // when N is wide.  QI_HIP_FP6_TILES (0, 3 or 4) overrides the choice,
-    // for tuning.
+    // when N is wide.  QI_HIP_FP6_TILES (0, 3, 4, or 5 for one 128 x 128
+    // tile per workgroup) overrides the choice, for tuning.
     static const int forced = [] {
         const char *e = getenv("QI_HIP_FP6_TILES");
         return e ? atoi(e) : -1;
@@ -346,6 +555,11 @@ QI_API int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *w_codes6, cons
     if (forced >= 0) cfg = forced;
     switch (cfg) {
     case 0:
+        // The persistent kernel takes whole 128 x 128 tiles only.
+        if (m % 128 == 0 && n % 128 == 0)
+            return launch_fp6_persistent(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, s);
+        return launch_fp6<2, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, s);
+    case 5:
         return launch_fp6<2, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, s);
     case 3:
         return launch_fp6<1, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, s);

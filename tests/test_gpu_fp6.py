@@ -195,3 +195,45 @@ def test_fp6_group_partials_exact(dev):
         a6_g = _dev(set_fp6_scales(a6_host, m, k, s_act), dev)  # m is a multiple of 32
         got = ops.w4a4_gemm_fp6(a6_g, w6, m).cpu().numpy()
         np.testing.assert_array_equal(got, partials[:, :, g].astype(np.float32))
+
+
+# Shapes on the persistent 128 x 128 path (M, N multiples of 128, at least
+# 512 tiles).  With two workgroups on each of the MI355X's 256 CUs (512
+# slots): 768 tiles = one full round + 256 tiles run as 512 halves (XCD
+# pairing); 1856 tiles = several tiles per workgroup, no halves (320 left
+# over); 612 tiles = one round + 100 tiles as 200 halves (plain pairing).
+# K = 256 is one ring of groups per tile, so every ring switches tiles.
+@pytest.mark.parametrize("m,n,k", [(2048, 6144, 256), (2048, 6144, 768), (2048, 14848, 256), (512, 19584, 512)])
+def test_fp6_gemm_persistent_bit_exact(dev, m, n, k):
+    print(f"fp6 persistent gemm m={m} n={n} k={k}", flush=True)
+    import qwen_image_hip.ops as ops
+    x = heavy_tailed(m, k, 700 + k)
+    w = weights_f16(n, k, 701 + n)
+    ac, as_ = oracle.quantize_activations(x)
+    wc, ws, _ = oracle.quantize_matrix(w, 6, clip=True)
+    a6, _ = ops.quantize_activations_fp6(_dev(x, dev))
+    w6, _ = ops.relayout_w4a4_fp6(_dev(wc, dev), _h(ws, dev))
+    got = ops.w4a4_gemm_fp6(a6, w6, m).cpu().numpy()
+    want = oracle.w4a4_gemm(ac, as_, wc, ws)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_fp6_gemm_persistent_epilogue(dev):
+    """Bias + GELU + fp16 stores at every tile switch of the persistent path."""
+    import qwen_image_hip.ops as ops
+    m, n, k = 2048, 6144, 512
+    print(f"fp6 persistent epilogue m={m} n={n} k={k}", flush=True)
+    x = heavy_tailed(m, k, 710)
+    w = weights_f16(n, k, 711)
+    bias = np.random.default_rng(712).normal(0, 0.5, size=n).astype(np.float32)
+    ac, as_ = oracle.quantize_activations(x)
+    wc, ws, _ = oracle.quantize_matrix(w, 6, clip=True)
+    a6, _ = ops.quantize_activations_fp6(_dev(x, dev))
+    w6, _ = ops.relayout_w4a4_fp6(_dev(wc, dev), _h(ws, dev))
+    got = ops.w4a4_gemm_fp6(a6, w6, m, bias=_dev(bias, dev), out_dtype=torch.float16, gelu=True)
+    got = got.float().cpu().numpy()
+    v = oracle.gelu_tanh(oracle.w4a4_gemm(ac, as_, wc, ws) + bias[None, :])
+    want = oracle.half_to_f32(oracle.half_from_f32(v))
+    # fp16 output of a GELU on the hardware exp2 / reciprocal: within two
+    # fp16 ulps of the correctly rounded value.
+    np.testing.assert_allclose(got, want, rtol=2 * 2.0 ** -10, atol=2.0 ** -20)
