@@ -124,6 +124,18 @@ int qi_hip_w4a4_gemm_tiled(const void *a_codes, const void *a_scales, const void
 int qi_hip_w4a16_gemm_tiled(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
                             const float *bias, void *y, int out_type, int epilogue, int m, int n, int k,
                             void *stream);
+/* The same GEMM over a fused record: several records of one input (the
+ * reference's reuse_input group, transformer.cplus:759-762 -- to_q, to_k,
+ * to_v) concatenated along n at upload, so their n outputs are
+ * n / n_part consecutive parts of n_part outputs each, and y holds the parts
+ * as consecutive [m, n_part] arrays (q, then k, then v).  One launch in
+ * place of one per record.  n_part % 16 == 0, n % n_part == 0; n_part == n
+ * is qi_hip_w4a16_gemm_tiled.  The kernel shape is chosen for the fused n,
+ * so outputs agree with per-record calls within the W4A16 tolerance (bit
+ * for bit when the same kernel shape is chosen). */
+int qi_hip_w4a16_gemm_tiled_parts(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
+                                  const float *bias, void *y, int out_type, int epilogue, int m, int n, int k,
+                                  int n_part, void *stream);
 
 /* Bandwidth-bound W4A16 GEMV for 1 <= m <= 16 (the adaLN / timestep
  * modulation linears).  Same arithmetic and layouts as above.  The
@@ -160,6 +172,11 @@ int qi_hip_relayout_w4a4_fp6(const void *codes, const void *scales, void *codes6
  * aligned to 16 bytes (f32) or 8 bytes (f16). */
 int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *w_codes6, const float *bias, void *y, int out_type,
                          int epilogue, int m, int n, int k, void *stream);
+/* The fp6 W4A4 GEMM over a fused record (parts as for
+ * qi_hip_w4a16_gemm_tiled_parts; n_part % 32 == 0, n % n_part == 0).  Every
+ * output is bit-identical to the per-record call's. */
+int qi_hip_w4a4_gemm_fp6_parts(const void *a_codes6, const void *w_codes6, const float *bias, void *y,
+                               int out_type, int epilogue, int m, int n, int k, int n_part, void *stream);
 
 /* Device-side QIPACK quantiser (int4_pack.cplus:237-468 arithmetic, bit-exact):
  * w_half fp16 [n, k] -> QIPACK arrays.  scheme 5 = W4A16 affine (minimums

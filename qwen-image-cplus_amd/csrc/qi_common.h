@@ -241,6 +241,15 @@ __device__ __forceinline__ void store_out(void *y, size_t index, float v, int ou
         reinterpret_cast<float *>(y)[index] = v;
 }
 
+// Index of output (row, col) when y holds n / n_part consecutive [m, n_part]
+// arrays (a fused record's parts, e.g. q, k, v); n_part == n is the plain
+// [m, n] layout.  col0 is a wave-uniform column in the same part as col.
+__device__ __forceinline__ size_t out_index(int row, int col, int col0, int m, int n, int n_part) {
+    if (n_part == n) return static_cast<size_t>(row) * n + col;
+    const int part = static_cast<int>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(col0))) / n_part;
+    return static_cast<size_t>(part) * m * n_part + static_cast<size_t>(row) * n_part + (col - part * n_part);
+}
+
 __device__ __forceinline__ float epilogue(float v, const float *bias, int col, int epi) {
     if (bias) v += bias[col];
     if (epi == QI_HIP_EPILOGUE_GELU_TANH) v = gelu_tanh(v);

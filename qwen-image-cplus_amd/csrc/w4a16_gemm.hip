@@ -286,7 +286,7 @@ __device__ __forceinline__ void w4a16_group_mfma(const uint8_t *xs, const v2i (&
 template <int TM, int TN, int NW>
 __global__ __launch_bounds__(NW *WAVE, (NW >= 8 ? 1 : 2)) void w4a16_tiled_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
-    const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int m, int n, int k) {
+    const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int m, int n, int k, int n_part) {
     constexpr int NSTAGE = 4;
     constexpr int BM = TM * 16, BN = NW * TN * 16;
     constexpr int A_INSTR = BM / 8;  // 1 KiB = 8 rows x 128 bytes per direct load
@@ -382,7 +382,8 @@ __global__ __launch_bounds__(NW *WAVE, (NW >= 8 ? 1 : 2)) void w4a16_tiled_kerne
     // n-tile j, 4q + r.
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-        const int col = block_col + (wave * TN + j) * 16 + 4 * q;
+        const int col0 = block_col + (wave * TN + j) * 16;  // wave-uniform
+        const int col = col0 + 4 * q;
         if (col >= n) continue;
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
@@ -391,7 +392,7 @@ __global__ __launch_bounds__(NW *WAVE, (NW >= 8 ? 1 : 2)) void w4a16_tiled_kerne
             float v[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) v[r] = epilogue(acc[j][i][r], bias, col + r, epi);
-            const size_t idx = static_cast<size_t>(row) * n + col;
+            const size_t idx = out_index(row, col, col0, m, n, n_part);
             if (out_type == QI_HIP_OUT_F16) {
                 uint2 h;
                 h.x = static_cast<uint32_t>(f2h(v[0])) | (static_cast<uint32_t>(f2h(v[1])) << 16);
@@ -406,13 +407,13 @@ __global__ __launch_bounds__(NW *WAVE, (NW >= 8 ? 1 : 2)) void w4a16_tiled_kerne
 
 template <int TM, int TN, int NW>
 static int launch_tiled(const void *x, const void *codes, const void *scales, const float *bias, void *y,
-                        int out_type, int epi, int m, int n, int k, hipStream_t stream) {
+                        int out_type, int epi, int m, int n, int k, int n_part, hipStream_t stream) {
     constexpr int BM = TM * 16, BN = NW * TN * 16;
     const long long blocks = static_cast<long long>((m + BM - 1) / BM) * ((n + BN - 1) / BN);
     if (blocks > 0x7FFFFFFFLL) return kInvalid;
     w4a16_tiled_kernel<TM, TN, NW><<<dim3(static_cast<unsigned>(blocks)), dim3(NW * WAVE), 0, stream>>>(
         static_cast<const uint16_t *>(x), static_cast<const uint8_t *>(codes), static_cast<const uint16_t *>(scales),
-        bias, y, out_type, epi, m, n, k);
+        bias, y, out_type, epi, m, n, k, n_part);
     return launch_status();
 }
 
@@ -429,7 +430,7 @@ static int launch_tiled(const void *x, const void *codes, const void *scales, co
 template <int TM, int TN>
 __global__ __launch_bounds__(4 * WAVE) void w4a16_splitk_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
-    const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int m, int n, int k) {
+    const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int m, int n, int k, int n_part) {
     constexpr int NW = 4, NSTAGE = 4;
     constexpr int BM = TM * 16, BN = TN * 16;
     constexpr int A_PER_W = BM / 8;  // 1 KiB direct loads: rows 8u .. 8u+7
@@ -531,11 +532,12 @@ __global__ __launch_bounds__(4 * WAVE) void w4a16_splitk_kernel(
         // acc[j][i][r] = y[row, col]: row = m-tile i, lane % 16; col = n-tile
         // j, 4 (lane / 16) + r.
         const int ln = pos % WAVE, ji = pos / WAVE, i = ji % TM, j = ji / TM;
-        const int row = block_row + 16 * i + (ln & 15), col = block_col + 16 * j + 4 * (ln >> 4);
+        const int col0 = block_col + 16 * j;  // wave-uniform: pos / WAVE is
+        const int row = block_row + 16 * i + (ln & 15), col = col0 + 4 * (ln >> 4);
         if (row >= m || col >= n) continue;
         const float vv[4] = {epilogue(v.x, bias, col, epi), epilogue(v.y, bias, col + 1, epi),
                              epilogue(v.z, bias, col + 2, epi), epilogue(v.w, bias, col + 3, epi)};
-        const size_t idx = static_cast<size_t>(row) * n + col;
+        const size_t idx = out_index(row, col, col0, m, n, n_part);
         if (out_type == QI_HIP_OUT_F16) {
             uint2 h;
             h.x = static_cast<uint32_t>(f2h(vv[0])) | (static_cast<uint32_t>(f2h(vv[1])) << 16);
@@ -549,13 +551,13 @@ __global__ __launch_bounds__(4 * WAVE) void w4a16_splitk_kernel(
 
 template <int TM, int TN>
 static int launch_splitk(const void *x, const void *codes, const void *scales, const float *bias, void *y,
-                         int out_type, int epi, int m, int n, int k, hipStream_t stream) {
+                         int out_type, int epi, int m, int n, int k, int n_part, hipStream_t stream) {
     constexpr int BM = TM * 16, BN = TN * 16;
     const long long blocks = static_cast<long long>((m + BM - 1) / BM) * ((n + BN - 1) / BN);
     if (blocks > 0x7FFFFFFFLL) return kInvalid;
     w4a16_splitk_kernel<TM, TN><<<dim3(static_cast<unsigned>(blocks)), dim3(4 * WAVE), 0, stream>>>(
         static_cast<const uint16_t *>(x), static_cast<const uint8_t *>(codes), static_cast<const uint16_t *>(scales),
-        bias, y, out_type, epi, m, n, k);
+        bias, y, out_type, epi, m, n, k, n_part);
     return launch_status();
 }
 
@@ -598,19 +600,31 @@ QI_API int qi_w4a16_gemm(const void *x_half, const void *codes, const void *scal
                            nullptr);
 }
 
-QI_API int qi_hip_w4a16_gemm_tiled(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
-                                   const float *bias, void *y, int out_type, int epilogue, int m, int n, int k,
-                                   void *stream) {
+QI_API int qi_hip_w4a16_gemm_tiled_parts(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
+                                         const float *bias, void *y, int out_type, int epilogue, int m, int n, int k,
+                                         int n_part, void *stream) {
     if (m <= 0 || n <= 0 || k <= 0 || n % 16 || k % 64) return kInvalid;
+    if (n_part <= 0 || n_part % 16 || n % n_part) return kInvalid;
     if (!x_half || !w_tiled_codes || !w_tiled_scales || !y) return kInvalid;
     if (out_type != QI_HIP_OUT_F32 && out_type != QI_HIP_OUT_F16) return kInvalid;
     if (epilogue != QI_HIP_EPILOGUE_NONE && epilogue != QI_HIP_EPILOGUE_GELU_TANH) return kInvalid;
     if (reinterpret_cast<uintptr_t>(x_half) % 16 || reinterpret_cast<uintptr_t>(w_tiled_codes) % 8 ||
         reinterpret_cast<uintptr_t>(w_tiled_scales) % 4 || k % 8)
         return kInvalid;
-    if (m <= 16)
-        return qi_hip_w4a16_gemv_impl(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
-                                      stream_of(stream));
+    if (m <= 16) {
+        // One GEMV per part: a part is n_part / 16 whole weight tiles.
+        const size_t tile_codes = static_cast<size_t>(k / 64) * 64 * 8, tile_scales = static_cast<size_t>(k / 64) * 64;
+        const size_t out_bytes = static_cast<size_t>(m) * n_part * (out_type == QI_HIP_OUT_F16 ? 2 : 4);
+        for (int p = 0; p < n / n_part; ++p) {
+            const size_t tiles = static_cast<size_t>(p) * (n_part / 16);
+            const int st = qi_hip_w4a16_gemv_impl(
+                x_half, static_cast<const uint8_t *>(w_tiled_codes) + tiles * tile_codes,
+                static_cast<const uint8_t *>(w_tiled_scales) + tiles * tile_scales, bias ? bias + p * n_part : nullptr,
+                static_cast<uint8_t *>(y) + p * out_bytes, out_type, epilogue, m, n_part, k, stream_of(stream));
+            if (st) return st;
+        }
+        return 0;
+    }
     if (static_cast<long long>(m) * k * 2 >= (1LL << 32) || static_cast<long long>(n) * (k / 2) >= (1LL << 32))
         return kInvalid;
     // Small m: short row tiles so the grid still covers the 256 CUs.
@@ -620,23 +634,30 @@ QI_API int qi_hip_w4a16_gemm_tiled(const void *x_half, const void *w_tiled_codes
     // -> 17.5 us, 256 x 3072 x 12288 67.4 -> 49.3 us; wider N keeps the tiled
     // kernel).
     if (m <= 256 && static_cast<long long>((m + 31) / 32) * ((n + 63) / 64) < 1024)
-        return launch_splitk<4, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
+        return launch_splitk<4, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k, n_part,
                                    stream_of(stream));
     if (m <= 256)
-        return launch_tiled<2, 1, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
+        return launch_tiled<2, 1, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k, n_part,
                                      stream_of(stream));
     if (m <= 1024)
-        return launch_tiled<4, 1, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
+        return launch_tiled<4, 1, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k, n_part,
                                      stream_of(stream));
     // 256 x 256 tiles (eight waves, one workgroup per CU: each weight is
     // dequantised for twice the rows) when they still give three or more
     // workgroups per CU; measured 11 % faster at 4096 x 12288 x 3072.
     if (n % 256 == 0 && static_cast<long long>((m + 255) / 256) * (n / 256) >= 768)
-        return launch_tiled<16, 2, 8>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
+        return launch_tiled<16, 2, 8>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k, n_part,
                                       stream_of(stream));
     if (n % 192 == 0)
-        return launch_tiled<8, 3, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
+        return launch_tiled<8, 3, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k, n_part,
                                      stream_of(stream));
-    return launch_tiled<8, 2, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
+    return launch_tiled<8, 2, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k, n_part,
                                  stream_of(stream));
+}
+
+QI_API int qi_hip_w4a16_gemm_tiled(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
+                                   const float *bias, void *y, int out_type, int epilogue, int m, int n, int k,
+                                   void *stream) {
+    return qi_hip_w4a16_gemm_tiled_parts(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
+                                         n, stream);
 }

@@ -80,8 +80,8 @@ struct Fp6Shape {
 template <int TM, int TN, int WM, int WN, int NSTAGE, bool WHOLE, typename Map>
 __device__ __forceinline__ void fp6_tiles(uint8_t *lds, const uint8_t *__restrict__ a6,
                                           const uint8_t *__restrict__ w6, const float *__restrict__ bias,
-                                          void *__restrict__ y, int out_type, int epi, int m, int n, int k, int count,
-                                          Map map) {
+                                          void *__restrict__ y, int out_type, int epi, int m, int n, int k, int n_part,
+                                          int count, Map map) {
     using S = Fp6Shape<TM, TN, WM, WN, NSTAGE>;
     constexpr int NW = WM * WN;
     constexpr int MT = S::MT, NTL = S::NTL;
@@ -244,7 +244,7 @@ __device__ __forceinline__ void fp6_tiles(uint8_t *lds, const uint8_t *__restric
                     float v[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) v[r] = epilogue(acc[j][i][4 * a + r], bias, col + r, epi);
-                    const size_t idx = static_cast<size_t>(row) * n + col;
+                    const size_t idx = out_index(row, col, tile_col, m, n, n_part);
                     if (out_type == QI_HIP_OUT_F16) {
                         uint2 h;
                         h.x = static_cast<uint32_t>(f2h(v[0])) | (static_cast<uint32_t>(f2h(v[1])) << 16);
@@ -395,13 +395,13 @@ __device__ __forceinline__ void fp6_tiles(uint8_t *lds, const uint8_t *__restric
 template <int TM, int TN, int WM, int WN, int NSTAGE>
 __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2))) void w4a4_fp6_kernel(
     const uint8_t *__restrict__ a6, const uint8_t *__restrict__ w6, const float *__restrict__ bias,
-    void *__restrict__ y, int out_type, int epi, int m, int n, int k) {
+    void *__restrict__ y, int out_type, int epi, int m, int n, int k, int n_part) {
     using S = Fp6Shape<TM, TN, WM, WN, NSTAGE>;
     __shared__ __attribute__((aligned(16))) uint8_t lds[S::LDS_BYTES];
     const int tiles_m = (m + S::BM - 1) / S::BM, tiles_n = (n + S::BN - 1) / S::BN;
     int tm, tn;
     tile_of_block(blockIdx.x, tiles_m, tiles_n, 8, tm, tn);
-    fp6_tiles<TM, TN, WM, WN, NSTAGE, false>(lds, a6, w6, bias, y, out_type, epi, m, n, k, 1,
+    fp6_tiles<TM, TN, WM, WN, NSTAGE, false>(lds, a6, w6, bias, y, out_type, epi, m, n, k, n_part, 1,
                                       [&](int, int &mt0, int &nt0) {
                                           mt0 = tm * S::MT;
                                           nt0 = tn * S::NTL;
@@ -423,7 +423,8 @@ constexpr int FP6_MAX_TILES = 128;
 template <int TN, int WM, int WN, int NSTAGE>
 __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2))) void w4a4_fp6_persistent_kernel(
     const uint8_t *__restrict__ a6, const uint8_t *__restrict__ w6, const float *__restrict__ bias,
-    void *__restrict__ y, int out_type, int epi, int m, int n, int k, int full_tiles, int half_units) {
+    void *__restrict__ y, int out_type, int epi, int m, int n, int k, int n_part, int full_tiles,
+    int half_units) {
     static_assert(NSTAGE == 4, "tiles end on ring boundaries");
     using S2 = Fp6Shape<2, TN, WM, WN, NSTAGE>;
     using S1 = Fp6Shape<1, TN, WM, WN, NSTAGE>;
@@ -440,7 +441,7 @@ __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2)
     }
     __syncthreads();
     if (count > 0)
-        fp6_tiles<2, TN, WM, WN, NSTAGE, true>(lds, a6, w6, bias, y, out_type, epi, m, n, k, count,
+        fp6_tiles<2, TN, WM, WN, NSTAGE, true>(lds, a6, w6, bias, y, out_type, epi, m, n, k, n_part, count,
                                          [&](int j, int &mt0, int &nt0) {
                                              const uint32_t e = __builtin_amdgcn_readfirstlane(tile_list[j]);
                                              mt0 = static_cast<int>(e & 0xFFFFu);
@@ -460,7 +461,7 @@ __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2)
         }
         int tm, tn;
         tile_of_block(t, tiles_m, tiles_n, 8, tm, tn);
-        fp6_tiles<1, TN, WM, WN, NSTAGE, false>(lds, a6, w6, bias, y, out_type, epi, m, n, k, 1,
+        fp6_tiles<1, TN, WM, WN, NSTAGE, false>(lds, a6, w6, bias, y, out_type, epi, m, n, k, n_part, 1,
                                          [&](int, int &mt0, int &nt0) {
                                              mt0 = tm * S2::MT + half * S1::MT;
                                              nt0 = tn * S1::NTL;
@@ -470,12 +471,12 @@ __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2)
 
 template <int TM, int TN, int WM, int WN, int NSTAGE>
 static int launch_fp6(const void *a6, const void *w6, const float *bias, void *y,
-                      int out_type, int epi, int m, int n, int k, hipStream_t stream) {
+                      int out_type, int epi, int m, int n, int k, int n_part, hipStream_t stream) {
     constexpr int BM = WM * TM * 32, BN = WN * TN * 32;
     const long long blocks = static_cast<long long>((m + BM - 1) / BM) * ((n + BN - 1) / BN);
     if (blocks > 0x7FFFFFFFLL) return kInvalid;
     w4a4_fp6_kernel<TM, TN, WM, WN, NSTAGE><<<dim3(static_cast<unsigned>(blocks)), dim3(WM * WN * WAVE), 0, stream>>>(
-        static_cast<const uint8_t *>(a6), static_cast<const uint8_t *>(w6), bias, y, out_type, epi, m, n, k);
+        static_cast<const uint8_t *>(a6), static_cast<const uint8_t *>(w6), bias, y, out_type, epi, m, n, k, n_part);
     return launch_status();
 }
 
@@ -494,7 +495,7 @@ static int device_cus() {
 
 // 128 x 128 tiles, two workgroups per CU, persistent (see the kernel).
 static int launch_fp6_persistent(const void *a6, const void *w6, const float *bias, void *y, int out_type, int epi,
-                                 int m, int n, int k, hipStream_t stream) {
+                                 int m, int n, int k, int n_part, hipStream_t stream) {
     const long long tiles = static_cast<long long>((m + 127) / 128) * ((n + 127) / 128);
     const long long slots = 2LL * device_cus();
     long long full = tiles, halves = 0, grid;
@@ -514,7 +515,7 @@ static int launch_fp6_persistent(const void *a6, const void *w6, const float *bi
     }
     if (tiles > 0x7FFFFFFFLL || (full + grid - 1) / grid > FP6_MAX_TILES) return kInvalid;
     w4a4_fp6_persistent_kernel<2, 2, 2, 4><<<dim3(static_cast<unsigned>(grid)), dim3(4 * WAVE), 0, stream>>>(
-        static_cast<const uint8_t *>(a6), static_cast<const uint8_t *>(w6), bias, y, out_type, epi, m, n, k,
+        static_cast<const uint8_t *>(a6), static_cast<const uint8_t *>(w6), bias, y, out_type, epi, m, n, k, n_part,
         static_cast<int>(full), static_cast<int>(halves));
     return launch_status();
 }
@@ -523,9 +524,10 @@ static int launch_fp6_persistent(const void *a6, const void *w6, const float *bi
 
 using namespace qi;
 
-QI_API int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *w_codes6, const float *bias, void *y,
-                                int out_type, int epilogue, int m, int n, int k, void *stream) {
+QI_API int qi_hip_w4a4_gemm_fp6_parts(const void *a_codes6, const void *w_codes6, const float *bias, void *y,
+                                      int out_type, int epilogue, int m, int n, int k, int n_part, void *stream) {
     if (m <= 0 || n <= 0 || k <= 0 || n % 32 || k % 256) return kInvalid;
+    if (n_part <= 0 || n_part % 32 || n % n_part) return kInvalid;
     if (!a_codes6 || !w_codes6 || !y) return kInvalid;
     if (out_type != QI_HIP_OUT_F32 && out_type != QI_HIP_OUT_F16) return kInvalid;
     if (epilogue != QI_HIP_EPILOGUE_NONE && epilogue != QI_HIP_EPILOGUE_GELU_TANH) return kInvalid;
@@ -557,15 +559,20 @@ QI_API int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *w_codes6, cons
     case 0:
         // The persistent kernel takes whole 128 x 128 tiles only.
         if (m % 128 == 0 && n % 128 == 0)
-            return launch_fp6_persistent(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, s);
-        return launch_fp6<2, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, s);
+            return launch_fp6_persistent(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, s);
+        return launch_fp6<2, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, s);
     case 5:
-        return launch_fp6<2, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, s);
+        return launch_fp6<2, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, s);
     case 3:
-        return launch_fp6<1, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, s);
+        return launch_fp6<1, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, s);
     case 4:
-        return launch_fp6<1, 1, 1, 1, 8>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, s);
+        return launch_fp6<1, 1, 1, 1, 8>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, s);
     default:
-        return launch_fp6<2, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, s);
+        return launch_fp6<2, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, s);
     }
+}
+
+QI_API int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *w_codes6, const float *bias, void *y,
+                                int out_type, int epilogue, int m, int n, int k, void *stream) {
+    return qi_hip_w4a4_gemm_fp6_parts(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n, stream);
 }

@@ -51,6 +51,26 @@ class PackedLinear:
     tiled_scales: torch.Tensor | None  # None for fp6 operands (scales inside the code blocks)
     bias: torch.Tensor | None = None  # fp32 [n] or None (the reference has none)
     operand: str = W4A4_FP6  # W4A4 records only
+    parts: int = 1  # > 1: records fused along n (fuse()); outputs [parts, rows, n / parts]
+
+    @classmethod
+    def fuse(cls, records: "list[PackedLinear]") -> "PackedLinear":
+        """One record for several records that read the same input (the
+        reference's reuse_input group: to_q, to_k, to_v after one
+        quantisation, transformer.cplus:759-762), concatenated along n so
+        one GEMM launch computes all of them.  The tiled layouts are per
+        16- or 32-row tile, so the fused arrays are the concatenations.
+        """
+        first = records[0]
+        for r in records:
+            if (r.scheme, r.n, r.k, r.operand, r.parts) != (first.scheme, first.n, first.k, first.operand, 1):
+                raise ValueError("fused records need one scheme, shape and operand format")
+            if (r.bias is None) != (first.bias is None):
+                raise ValueError("either every fused record has a bias or none has")
+        tc = torch.cat([r.tiled_codes for r in records], 0)
+        ts = None if first.tiled_scales is None else torch.cat([r.tiled_scales for r in records], 0)
+        bias = None if first.bias is None else torch.cat([r.bias for r in records], 0)
+        return cls(first.scheme, first.n * len(records), first.k, tc, ts, bias, first.operand, len(records))
 
     @classmethod
     def from_qipack(cls, scheme: int, codes: torch.Tensor, scales: torch.Tensor,
@@ -130,8 +150,10 @@ def linear(record: PackedLinear, work: Work, input: torch.Tensor, output: torch.
 
     ``input`` is fp32 (the engine's activations) or fp16.  ``reuse_input``
     skips the quantisation / conversion when the previous linear already
-    processed the same input (Q/K/V and gate/up in the reference).
+    processed the same input (Q/K/V and gate/up in the reference).  A fused
+    record (``PackedLinear.fuse``) writes ``output[parts, rows, N / parts]``.
     """
+    n_part = record.n // record.parts if record.parts > 1 else None
     rows = input.shape[0] if rows is None else rows
     k = record.k
     if input.shape[-1] != k:
@@ -141,7 +163,9 @@ def linear(record: PackedLinear, work: Work, input: torch.Tensor, output: torch.
         codes6 = work.fp6_views(rows, k)
         if not reuse_input:
             ops.quantize_activations_fp6(input[:rows], codes6)
-        return ops.w4a4_gemm_fp6(codes6, record.tiled_codes, rows, record.bias, out_dtype, gelu, output)
+        return ops.w4a4_gemm_fp6(codes6, record.tiled_codes, rows, record.bias, out_dtype, gelu, output, n_part)
+    if record.parts > 1 and record.scheme == SCHEME_W4A4_H256:
+        raise ValueError("fused W4A4 records run on the fp6 operand format")
     if record.scheme == SCHEME_W4A4_H256:
         if not reuse_input:
             ops.quantize_activations(input[:rows], codes, code_scales)
@@ -155,5 +179,5 @@ def linear(record: PackedLinear, work: Work, input: torch.Tensor, output: torch.
                 ops.f32_to_f16(input[:rows], halves)
             x_half = halves
         return ops.w4a16_gemm(x_half, record.tiled_codes, record.tiled_scales, record.bias, out_dtype, gelu,
-                              output)
+                              output, n_part)
     raise ValueError(f"unsupported scheme {record.scheme}")

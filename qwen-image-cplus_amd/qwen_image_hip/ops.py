@@ -166,14 +166,25 @@ def w4a4_gemm(a_codes, a_scales, w_tiled_codes, w_tiled_scales, bias=None, out_d
     return y
 
 
-def w4a16_gemm(x_half, w_tiled_codes, w_tiled_scales, bias=None, out_dtype=torch.float32, gelu=False, y=None):
+def _out_shape(m: int, n: int, n_part: int | None):
+    if n_part is None or n_part == n:
+        return (m, n)
+    if n_part <= 0 or n % n_part:
+        raise ValueError(f"n_part {n_part} does not divide n {n}")
+    return (n // n_part, m, n_part)
+
+
+def w4a16_gemm(x_half, w_tiled_codes, w_tiled_scales, bias=None, out_dtype=torch.float32, gelu=False, y=None,
+               n_part=None):
+    """y = x . W^T for tiled W4A16 weights; with n_part, y is [n / n_part, m, n_part]
+    (the parts of a fused record, qi_hip_w4a16_gemm_tiled_parts)."""
     m, k = x_half.shape
     n = w_tiled_codes.shape[0]
     out_type = OUT_F16 if out_dtype == torch.float16 else OUT_F32
-    y = y if y is not None else _empty((m, n), out_dtype, x_half)
-    st = load().qi_hip_w4a16_gemm_tiled(_ptr(x_half), _ptr(w_tiled_codes), _ptr(w_tiled_scales), _ptr(bias),
-                                        _ptr(y), out_type, EPILOGUE_GELU_TANH if gelu else EPILOGUE_NONE, m, n, k,
-                                        _stream())
+    y = y if y is not None else _empty(_out_shape(m, n, n_part), out_dtype, x_half)
+    st = load().qi_hip_w4a16_gemm_tiled_parts(_ptr(x_half), _ptr(w_tiled_codes), _ptr(w_tiled_scales), _ptr(bias),
+                                              _ptr(y), out_type, EPILOGUE_GELU_TANH if gelu else EPILOGUE_NONE, m, n,
+                                              k, n if n_part is None else n_part, _stream())
     check(st, "w4a16 gemm")
     return y
 
@@ -235,11 +246,15 @@ def relayout_w4a4_fp6(codes: torch.Tensor, scales: torch.Tensor, want_scales: bo
     return c6, ts
 
 
-def w4a4_gemm_fp6(a_codes6, w_codes6, m: int, bias=None, out_dtype=torch.float32, gelu=False, y=None):
+def w4a4_gemm_fp6(a_codes6, w_codes6, m: int, bias=None, out_dtype=torch.float32, gelu=False, y=None,
+                  n_part=None):
+    """fp6-operand W4A4 GEMM; with n_part, y is [n / n_part, m, n_part]
+    (qi_hip_w4a4_gemm_fp6_parts)."""
     n, k = w_codes6.shape[0], w_codes6.shape[1] // 56 * GROUP
     out_type = OUT_F16 if out_dtype == torch.float16 else OUT_F32
-    y = y if y is not None else _empty((m, n), out_dtype, w_codes6)
-    st = load().qi_hip_w4a4_gemm_fp6(_ptr(a_codes6), _ptr(w_codes6), _ptr(bias), _ptr(y), out_type,
-                                     EPILOGUE_GELU_TANH if gelu else EPILOGUE_NONE, m, n, k, _stream())
+    y = y if y is not None else _empty(_out_shape(m, n, n_part), out_dtype, w_codes6)
+    st = load().qi_hip_w4a4_gemm_fp6_parts(_ptr(a_codes6), _ptr(w_codes6), _ptr(bias), _ptr(y), out_type,
+                                           EPILOGUE_GELU_TANH if gelu else EPILOGUE_NONE, m, n, k,
+                                           n if n_part is None else n_part, _stream())
     check(st, "w4a4 gemm")
     return y

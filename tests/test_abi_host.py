@@ -67,6 +67,12 @@ def test_extension_argument_checks():
     # misaligned operand pointers are refused, not faulted on
     assert L.qi_hip_w4a4_gemm_tiled(9, 8, 8, 8, None, 8, 0, 0, 5, 32, 256, None) == INVALID
     assert L.qi_w4a4_quantize_activations(18, 16, 16, 4, 256) == INVALID
+    # fused-record parts: n_part must divide n and keep whole tiles
+    assert L.qi_hip_w4a4_gemm_fp6_parts(16, 16, None, 16, 0, 0, 4, 96, 256, 48, None) == INVALID
+    assert L.qi_hip_w4a4_gemm_fp6_parts(16, 16, None, 16, 0, 0, 4, 96, 256, 64, None) == INVALID
+    assert L.qi_hip_w4a4_gemm_fp6_parts(16, 16, None, 16, 0, 0, 4, 96, 256, 0, None) == INVALID
+    assert L.qi_hip_w4a16_gemm_tiled_parts(16, 8, 8, None, 8, 0, 0, 5, 96, 64, 24, None) == INVALID
+    assert L.qi_hip_w4a16_gemm_tiled_parts(16, 8, 8, None, 8, 0, 0, 5, 96, 64, 64, None) == INVALID
     # null pointers
     assert L.qi_w4a4_gemm(None, None, None, None, None, 128, 128, 256) == INVALID
 

@@ -237,3 +237,22 @@ def test_fp6_gemm_persistent_epilogue(dev):
     # fp16 output of a GELU on the hardware exp2 / reciprocal: within two
     # fp16 ulps of the correctly rounded value.
     np.testing.assert_allclose(got, want, rtol=2 * 2.0 ** -10, atol=2.0 ** -20)
+
+
+@pytest.mark.parametrize("m", [7, 300, 4096])
+def test_fused_qkv_record_matches_separate_records(dev, m):
+    """A fused (q, k, v) record writes each part bit-identical to the part's
+    own call (the reference's to_q / to_k / to_v with reuse_input)."""
+    import qwen_image_hip as q
+    n, k = 1024, 768  # m = 4096: 768 fused 128 x 128 tiles, the persistent kernel
+    print(f"fp6 fused qkv m={m} n={n} k={k}", flush=True)
+    x = _dev(heavy_tailed(m, k, 720 + m), dev)
+    recs = [q.PackedLinear.from_fp16(q.SCHEME_W4A4_H256, _dev(weights_f16(n, k, 721 + i), dev).view(torch.float16),
+                                     clip=True) for i in range(3)]
+    fused = q.PackedLinear.fuse(recs)
+    work = q.Work(m, k, dev)
+    got = q.linear(fused, work, x, out_dtype=torch.float16, gelu=True)
+    assert got.shape == (3, m, n)
+    for i, r in enumerate(recs):
+        want = q.linear(r, work, x, reuse_input=True, out_dtype=torch.float16, gelu=True)
+        torch.testing.assert_close(got[i], want, rtol=0, atol=0)

@@ -331,3 +331,25 @@ def test_linear_from_qipack_file(dev, tmp_path, scheme):
     a = q.linear(direct, work, x).cpu().numpy()
     b = q.linear(loaded, work, x).cpu().numpy()
     np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("m", [2, 300, 4096])
+def test_w4a16_fused_record_matches_separate_records(dev, m):
+    """A fused (q, k, v) W4A16 record: each part within the W4A16 tolerance of
+    the part's own call, and bit-identical on the GEMV path (m <= 16), which
+    runs the same kernel per part."""
+    import qwen_image_hip as q
+    n, k = 1024, 640
+    print(f"w4a16 fused qkv m={m} n={n} k={k}", flush=True)
+    x = _h(f16_bits(normal_f32(m, k, 730 + m)), dev)
+    recs = [q.PackedLinear.from_fp16(q.SCHEME_W4A16, _h(weights_f16(n, k, 731 + i), dev)) for i in range(3)]
+    fused = q.PackedLinear.fuse(recs)
+    work = q.Work(m, k, dev)
+    got = q.linear(fused, work, x, out_dtype=torch.float32)
+    assert got.shape == (3, m, n)
+    for i, r in enumerate(recs):
+        want = q.linear(r, work, x, out_dtype=torch.float32)
+        if m <= 16:
+            torch.testing.assert_close(got[i], want, rtol=0, atol=0)
+        else:
+            _close(got[i].cpu().numpy(), want.cpu().numpy())
