@@ -319,6 +319,80 @@ def bench_gemv(iters=200):
     return out
 
 
+STACK_STREAMS = {"image": 3 * 4096, "text": 512}  # config 5: 1024^2 edit with 2 reference images
+STACK_BLOCKS = 60
+
+
+def bench_stack(blocks=STACK_BLOCKS, steps=4):
+    """Config 5: the full 60-block MMDiT linear stack, W4A4 H256 g64, image
+    stream M=12288 + text stream M=512, every block with its own random-init
+    weights packed by the device QIPACK quantiser (fp6 operand records, Q/K/V
+    fused), heavy-tailed fp16 activations quantised online before every
+    distinct input.  The block inputs are the same buffers in every block
+    (their values do not change the work).  One denoising step = the 60
+    blocks; `steps` steps are timed one by one with HIP events, the first
+    reported separately as the warm-up."""
+    import torch
+    import qwen_image_hip as q
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(500)
+    layers = []
+    for _ in range(blocks):
+        blk = {}
+        for stream in STACK_STREAMS:
+            qkv = []
+            for name, n, k in block_shapes():
+                w = (torch.randn((n, k), generator=g, device="cuda") * 0.02).half()
+                rec = q.PackedLinear.from_fp16(q.SCHEME_W4A4_H256, w, clip=True)
+                del w
+                if name in ("to_q", "to_k", "to_v"):
+                    qkv.append(rec)
+                else:
+                    blk[(stream, name)] = rec
+            blk[(stream, "qkv")] = q.PackedLinear.fuse(qkv)
+            del qkv
+        layers.append(blk)
+    bufs = {}
+    for stream, m in STACK_STREAMS.items():
+        bufs[stream] = {
+            "x_qkv": heavy_tailed(m, HIDDEN, g), "x_out": heavy_tailed(m, HIDDEN, g),
+            "x_mlp": heavy_tailed(m, HIDDEN, g), "work": q.Work(m, MLP, "cuda"),
+            "y": torch.empty((m, HIDDEN), dtype=torch.float16, device="cuda"),
+            "qkv": torch.empty((3, m, HIDDEN), dtype=torch.float16, device="cuda"),
+            "h": torch.empty((m, MLP), dtype=torch.float16, device="cuda"),
+        }
+    torch.cuda.synchronize()
+    lin, f16 = q.linear, torch.float16
+
+    def denoise_step():
+        for blk in layers:
+            for stream in STACK_STREAMS:
+                b, w = bufs[stream], bufs[stream]["work"]
+                lin(blk[(stream, "qkv")], w, b["x_qkv"], b["qkv"], out_dtype=f16)
+                lin(blk[(stream, "to_out")], w, b["x_out"], b["y"], out_dtype=f16)
+                lin(blk[(stream, "mlp_up")], w, b["x_mlp"], b["h"], out_dtype=f16, gelu=True)
+                lin(blk[(stream, "mlp_down")], w, b["h"], b["y"], out_dtype=f16)
+
+    times = []
+    for _ in range(steps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        denoise_step()
+        e1.record()
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1))
+    ops_step = blocks * 2.0 * sum(n * k for _, n, k in block_shapes()) * sum(STACK_STREAMS.values())
+    ms = sum(times[1:]) / max(1, len(times) - 1)
+    tops = ops_step / (ms * 1e-3) / 1e12
+    del layers, bufs
+    torch.cuda.empty_cache()
+    return {"workload": f"config 5: {blocks}-block W4A4 stack, image M={STACK_STREAMS['image']} + text "
+                        f"M={STACK_STREAMS['text']}", "ms_per_step": round(ms, 3),
+            "first_step_ms": round(times[0], 3), "TOPS": round(tops, 1),
+            "frac_int8_peak": round(tops * 1e12 / PEAK_INT8_OPS, 4), "steps_timed": len(times) - 1}
+
+
 def cpu_baseline(budget_s=20.0):
     """The CPU oracle (C, OpenMP over the host cores) on a bounded sample of
     the same workload: the block's W4A4 linears (quantise + GEMM per linear,
@@ -365,6 +439,8 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="only the headline W4A4 block")
+    ap.add_argument("--no-stack", action="store_true", help="skip the 60-block stack (config 5)")
+    ap.add_argument("--stack-only", action="store_true", help="only the 60-block stack (config 5), printed as JSON")
     ap.add_argument("--no-graph", action="store_true", help="time the eager step (one Python call per linear)")
     ap.add_argument("--two-streams", action="store_true",
                     help="run each phase's text-stream linears on a second HIP stream beside the image stream's "
@@ -385,6 +461,9 @@ def main(argv=None) -> int:
     torch.cuda.set_device(0)
     if args.kernel_only:
         return kernel_only()
+    if args.stack_only:
+        print(json.dumps(bench_stack()), flush=True)
+        return 0
     log("packing W4A4 block weights (fp6 operands)")
     blk4 = Block(q.SCHEME_W4A4_H256, 1)
     step4 = StepW4A4(blk4, 2, one_stream=not args.two_streams)
@@ -466,6 +545,10 @@ def main(argv=None) -> int:
         torch.cuda.empty_cache()
         extra["modulation_gemv"] = bench_gemv()
         log(f"gemv: {extra['modulation_gemv']}")
+        if not args.no_stack:
+            log("packing the 60-block stack (config 5)")
+            extra["stack60_w4a4"] = bench_stack()
+            log(f"stack: {extra['stack60_w4a4']}")
 
     cpu = None
     if not args.no_cpu:
