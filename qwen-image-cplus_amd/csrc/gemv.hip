@@ -1,23 +1,22 @@
 // W4A16 GEMV for 1 <= m <= 16 rows: the adaLN / timestep modulation linears,
-// whose cost is reading the int4 weights once from HBM.
+// whose cost is reading the int4 weights once from HBM.  The reference runs
+// these linears in BF16 through cuBLAS SGEMM
+// (qwen_image_cuda/src/transformer.cplus:716-730); there is no INT4 GEMV there
+// to follow, so the arithmetic is the W4A16 GEMM's weights
+// (qwen_image_cuda/cuda/gemm.cu:222-230) within the W4A16 tolerance.
 //
-// Arithmetic: W = fp16(fmaf(code, scale, minimum)) exactly as the W4A16 GEMM
-// (qwen_image_cuda/cuda/gemm.cu:222-230), computed two weights per packed
-// fp16 instruction where that is provably the same value; weight x activation
-// pairs accumulate in fp32 on the matrix core (v_mfma_f32_16x16x32_f16: the
-// tiled code layout is already its A-operand layout).  The reference runs these linears in BF16 through
-// cuBLAS SGEMM (qwen_image_cuda/src/transformer.cplus:716-730); there is no
-// INT4 GEMV there to follow.
-//
-// Design.  One workgroup owns one 16-row weight tile; in the tiled layout the
+// Layout: one workgroup owns one 16-row weight tile; in the tiled layout the
 // tile's groups are consecutive 512-byte blocks, and each of the four
-// wavefronts streams a contiguous quarter of them, keeping two batches of
-// four groups of loads (one 8-byte code load and one scale pair per lane
-// each) in flight.
-// The activations are first staged in LDS, so the weight stream never waits
-// on them.  Each lane dequantises its 16 weights per group, two MFMAs per
-// group multiply them with up to 16 rows of x, and the wavefronts' partial
-// sums are added through LDS.
+// wavefronts streams a contiguous quarter of them, with batches of groups of
+// loads (one 8-byte code load and one scale pair per lane each) in flight.
+// The activations are staged in LDS, and the wavefronts' partial sums are
+// added through LDS.  Three kernels:
+//   * w4a16_gemv_dot2_kernel (m = 1, 2): vector unit, dot2 on the fp16
+//     integers 1024 + c with the factored per-group scale step;
+//   * w4a16_gemv_factored_kernel (m <= 16, x fits in LDS): the same
+//     factored form on the matrix core (16 rows per MFMA);
+//   * w4a16_gemv_kernel: dequantised fp16 weights (the GEMM's exact weights)
+//     on the matrix core, for x too large for LDS.
 
 #include "qi_common.h"
 
@@ -258,11 +257,143 @@ __global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_factored_kernel(
     }
 }
 
+// Vector-unit form for m <= 2 (the modulation linears' one or two rows),
+// where a 16-row MFMA would waste most of its work.  The factored arithmetic
+// of the kernel above, per lane: lane l of a 16-row tile holds 16 codes of
+// row l % 16 per group (elements 8q .. 8q+7 and 32+8q .. 32+8q+7, q = l / 16,
+// each pair (2i, 2i+1) one nibble-pair slot), inserts them into 0x6400 as the
+// fp16 integers 1024 + c, and forms P_l = sum x (1024 + c) over its 16
+// inputs with v_dot2_f32_f16 (fp16 products exact in fp32).  With X_l the sum
+// of the same 16 inputs (precomputed once per workgroup in LDS), the lane's
+// share of the group is s (P_l - 1024 X_l) + min X_l; the shares are summed
+// per lane over its groups, then over the four lanes of a row and the
+// workgroup's waves.  This is the group's dot product with the weights
+// c s + min in fp32, like the MFMA form: inside the W4A16 tolerance, and
+// bit-exact fp32(c s + min) on one-hot rows.
+template <int M>
+__global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_dot2_kernel(
+    const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
+    const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int n, int k) {
+    __shared__ float partial[GEMV_WAVES][M][16];
+    extern __shared__ __attribute__((aligned(16))) uint16_t xs_lds[];  // M * k fp16, then M * k / 16 fp32 sums
+    float *xsum = reinterpret_cast<float *>(xs_lds + M * k);
+    const int groups = k >> 6;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
+    const int q = lane >> 4, r16 = lane & 15;
+    const int tile = blockIdx.x;
+
+    const int per_wave = (groups + GEMV_WAVES - 1) / GEMV_WAVES;
+    const int g_begin = wave * per_wave;
+    const int g_end = min(groups, g_begin + per_wave);
+    const uint8_t *cp = codes + static_cast<size_t>(tile) * groups * 512 + lane * 8;
+    // The (scale, minimum) pair of the lane's own row.
+    const uint32_t *sp = reinterpret_cast<const uint32_t *>(scales) + static_cast<size_t>(tile) * groups * 16 + r16;
+
+    // Batches of three groups (measured faster than six on MI355X: the
+    // first groups' compute starts sooner).
+    constexpr int FB = 3;
+    uint2 c[2][FB];
+    uint32_t sc[2][FB];
+    const bool whole = groups % (GEMV_WAVES * 2 * FB) == 0;
+    auto load_batch = [&](int b, int g) {
+        if (whole && g >= g_end) return;
+#pragma unroll
+        for (int u = 0; u < FB; ++u) {
+            if (whole || g + u < g_end) {
+                const v2u t =
+                    __builtin_nontemporal_load(reinterpret_cast<const v2u *>(cp + static_cast<size_t>(g + u) * 512));
+                c[b][u] = uint2{t[0], t[1]};
+                sc[b][u] = __builtin_nontemporal_load(sp + static_cast<size_t>(g + u) * 16);
+            }
+        }
+    };
+    load_batch(0, g_begin);
+    load_batch(1, g_begin + FB);
+
+    const int chunks = M * k / 8;  // 16-byte chunks of x
+    for (int i = threadIdx.x; i < chunks; i += GEMV_WAVES * WAVE)
+        reinterpret_cast<uint4 *>(xs_lds)[i] = reinterpret_cast<const uint4 *>(x)[i];
+    __syncthreads();
+    // xsum[row][4 g + q] = sum of the row's inputs 64 g + 8q .. +7 and
+    // 64 g + 32 + 8q .. +7 (the 16 inputs a lane with that q reads).
+    for (int i = threadIdx.x; i < M * groups * 4; i += GEMV_WAVES * WAVE) {
+        const int row = i / (groups * 4), gq = i % (groups * 4), g = gq >> 2, qq = gq & 3;
+        const uint16_t *xr = xs_lds + static_cast<size_t>(row) * k + g * 64 + 8 * qq;
+        float t = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t += h2f(xr[e]) + h2f(xr[32 + e]);
+        xsum[i] = t;
+    }
+    __syncthreads();
+
+    uint32_t magic = 0x64006400u;
+    asm volatile("" : "+v"(magic));  // kept in a VGPR: lets the insert be one v_bfi_b32
+    float yacc[M];
+#pragma unroll
+    for (int r = 0; r < M; ++r) yacc[r] = 0.f;
+    auto consume = [&](int g, uint2 cc, uint32_t scq) {
+        v2h a[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            a[i] = __builtin_bit_cast(v2h, ((cc.x >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu));
+            a[4 + i] = __builtin_bit_cast(v2h, ((cc.y >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu));
+        }
+        const float sc_s = h2f(static_cast<uint16_t>(scq & 0xFFFFu)), sc_m = h2f(static_cast<uint16_t>(scq >> 16));
+#pragma unroll
+        for (int r = 0; r < M; ++r) {
+            const uint16_t *xr = xs_lds + static_cast<size_t>(r) * k + g * 64 + 8 * q;
+            const uint4 x0 = *reinterpret_cast<const uint4 *>(xr);
+            const uint4 x1 = *reinterpret_cast<const uint4 *>(xr + 32);
+            const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            float pl = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) pl = __builtin_amdgcn_fdot2(a[i], __builtin_bit_cast(v2h, xw[i]), pl, false);
+            const float xl = xsum[(r * groups + g) * 4 + q];
+            yacc[r] = __builtin_fmaf(sc_m, xl, yacc[r]);
+            yacc[r] = __builtin_fmaf(sc_s, __builtin_fmaf(-1024.0f, xl, pl), yacc[r]);
+        }
+    };
+    for (int g = g_begin; g < g_end; g += 2 * FB) {
+#pragma unroll
+        for (int u = 0; u < FB; ++u)
+            if (whole || g + u < g_end) consume(g + u, c[0][u], sc[0][u]);
+        load_batch(0, g + 2 * FB);
+#pragma unroll
+        for (int u = 0; u < FB; ++u)
+            if (whole || g + FB + u < g_end) consume(g + FB + u, c[1][u], sc[1][u]);
+        load_batch(1, g + 3 * FB);
+    }
+
+    // Sum the four lanes of a row (l, l + 16, l + 32, l + 48), then the waves.
+#pragma unroll
+    for (int r = 0; r < M; ++r) {
+        const float v = wave_sum16(yacc[r]);
+        if (q == 0) partial[wave][r][r16] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < M * 16) {
+        const int r = threadIdx.x >> 4, nn = threadIdx.x & 15;
+        float v = partial[0][r][nn];
+#pragma unroll
+        for (int w = 1; w < GEMV_WAVES; ++w) v += partial[w][r][nn];
+        const int col = tile * 16 + nn;
+        store_out(y, static_cast<size_t>(r) * n + col, epilogue(v, bias, col, epi), out_type);
+    }
+}
+
 static void launch_gemv(const uint16_t *x, const uint8_t *c, const uint16_t *s, const float *bias, void *y,
                         int out_type, int epi, int m, int n, int k, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(n / 16)), block(GEMV_WAVES * WAVE);
     const long long lds = static_cast<long long>(m) * k * 2;
-    if (lds <= GEMV_LDS_X)
+    // One or two rows: the vector-unit form (x and its 16-input sums in LDS).
+    const long long lds_dot2 = lds + static_cast<long long>(m) * (k / 16) * 4;
+    if (m == 1 && lds_dot2 <= GEMV_LDS_X)
+        w4a16_gemv_dot2_kernel<1><<<grid, block, static_cast<size_t>(lds_dot2), stream>>>(x, c, s, bias, y, out_type,
+                                                                                         epi, n, k);
+    else if (m == 2 && lds_dot2 <= GEMV_LDS_X)
+        w4a16_gemv_dot2_kernel<2><<<grid, block, static_cast<size_t>(lds_dot2), stream>>>(x, c, s, bias, y, out_type,
+                                                                                         epi, n, k);
+    else if (lds <= GEMV_LDS_X)
         w4a16_gemv_factored_kernel<<<grid, block, static_cast<size_t>(lds), stream>>>(x, c, s, bias, y, out_type, epi,
                                                                                       m, n, k);
     else

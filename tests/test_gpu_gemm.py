@@ -244,7 +244,7 @@ def _double_rounding_cases(count, seed=0):
     return s[idx], m[idx]
 
 
-@pytest.mark.parametrize("path", ["tiled", "reference", "gemv"])
+@pytest.mark.parametrize("path", ["tiled", "reference", "gemv", "gemv1", "gemv2"])
 def test_w4a16_dequant_bit_exact_identity(dev, path):
     """x = identity makes y = W^T exactly (one nonzero product per output), so
     the kernels' dequantised weights are compared bit for bit with the oracle,
@@ -266,8 +266,10 @@ def test_w4a16_dequant_bit_exact_identity(dev, path):
         if path == "tiled":
             got = ops.w4a16_gemm(_dev(eye, dev), tc, ts).cpu().numpy().T
         else:
-            got = np.concatenate([ops.w4a16_gemv(_dev(eye[r:r + 16], dev), tc, ts).cpu().numpy()
-                                  for r in range(0, k, 16)], axis=0).T
+            # 16 rows per call (matrix-core form); 1 or 2 rows (vector form)
+            rows = {"gemv": 16, "gemv1": 1, "gemv2": 2}[path]
+            got = np.concatenate([ops.w4a16_gemv(_dev(eye[r:r + rows], dev), tc, ts).cpu().numpy()
+                                  for r in range(0, k, rows)], axis=0).T
             # The GEMV keeps each weight c * s + minimum in fp32 (one
             # rounding of the exact value) instead of rounding it to fp16.
             nib = np.stack([codes & 15, codes >> 4], -1).reshape(n, k).astype(np.float64)
