@@ -319,6 +319,51 @@ def bench_gemv(iters=200):
     return out
 
 
+def bench_producers(iters=50):
+    """The producers in front of the quantiser at the image stream's shapes:
+    LayerNorm with modulation scale (M=4096, K=3072, fp32 hidden) and SwiGLU
+    (M=4096, K=12288, fp32 gate/up), each as the reference runs it (producer
+    kernel writing fp32, then the quantiser reading it back) and fused (one
+    quantiser pass applying the producer to what it loads)."""
+    import torch
+    from qwen_image_hip import ops
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(88)
+    m = STREAMS["image"]
+    out = {}
+    x = torch.randn((m, HIDDEN), generator=g, device="cuda") * 2.0
+    scale = torch.randn((2, HIDDEN), generator=g, device="cuda") * 0.3
+    normed = torch.empty_like(x)
+    codes = torch.empty((ops.fp6_rows(m), ops.fp6_row_bytes(MLP)), dtype=torch.uint8, device="cuda")
+    c3 = codes[:, : ops.fp6_row_bytes(HIDDEN)].contiguous()
+    stats = torch.empty((m, 2), dtype=torch.float32, device="cuda")
+
+    def ln_separate():
+        ops.layer_norm_scale(x, scale, 0, out=normed)
+        ops.quantize_activations_fp6(normed, c3)
+
+    def ln_fused():
+        ops.layer_norm_scale_quantize_fp6(x, scale, 0, c3, stats)
+
+    out["layer_norm_quantize"] = {"shape": f"{m}x{HIDDEN}", "separate_us": round(time_fn(ln_separate, iters, 5) * 1e3, 2),
+                                  "fused_us": round(time_fn(ln_fused, iters, 5) * 1e3, 2)}
+    gate = torch.randn((m, MLP), generator=g, device="cuda") * 3.0
+    up = torch.randn((m, MLP), generator=g, device="cuda")
+    act = torch.empty_like(gate)
+
+    def sw_separate():
+        ops.swiglu(gate, up, out=act)
+        ops.quantize_activations_fp6(act, codes)
+
+    def sw_fused():
+        ops.swiglu_quantize_fp6(gate, up, codes)
+
+    out["swiglu_quantize"] = {"shape": f"{m}x{MLP}", "separate_us": round(time_fn(sw_separate, iters, 5) * 1e3, 2),
+                              "fused_us": round(time_fn(sw_fused, iters, 5) * 1e3, 2)}
+    return out
+
+
 STACK_STREAMS = {"image": 3 * 4096, "text": 512}  # config 5: 1024^2 edit with 2 reference images
 STACK_BLOCKS = 60
 
@@ -545,6 +590,8 @@ def main(argv=None) -> int:
         torch.cuda.empty_cache()
         extra["modulation_gemv"] = bench_gemv()
         log(f"gemv: {extra['modulation_gemv']}")
+        extra["producers"] = bench_producers()
+        log(f"producers: {extra['producers']}")
         if not args.no_stack:
             log("packing the 60-block stack (config 5)")
             extra["stack60_w4a4"] = bench_stack()

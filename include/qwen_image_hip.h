@@ -178,6 +178,38 @@ int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *w_codes6, const float
 int qi_hip_w4a4_gemm_fp6_parts(const void *a_codes6, const void *w_codes6, const float *bias, void *y,
                                int out_type, int epilogue, int m, int n, int k, int n_part, void *stream);
 
+/* Producers fused with the activation quantiser.  The reference runs the
+ * LayerNorm-with-modulation-scale (qi_layer_norm_scale, ops.cu:56-59) and
+ * SwiGLU (qi_swiglu, ops.cu:141-144) as kernels writing fp32 activations
+ * that the quantiser then reads back (transformer.cplus:759-760, 808-813).
+ *
+ * qi_hip_layer_norm_scale: the reference's LayerNorm (affine-free, two-pass
+ * variance, eps 1e-6) times (1 + scale[i]) with scale row 1 (at
+ * scale + scale_stride) for rows < split and row 0 otherwise; fp32 or fp16
+ * (RNE) output -- the fp16 form is the W4A16 path's input conversion fused
+ * in.  width % 4 == 0; x, scale, out 16-byte aligned; scale_stride % 4 == 0.
+ *
+ * qi_hip_layer_norm_scale_quantize_fp6: the same values quantised straight
+ * into the fp6 operand layout of qi_hip_w4a4_quantize_activations_fp6
+ * (codes bit-identical to quantising qi_hip_layer_norm_scale's fp32
+ * output).  row_stats is caller scratch of m * 8 bytes (per row: mean and
+ * 1 / sqrt(variance + eps) as two floats).  k % 256 == 0.
+ *
+ * qi_hip_swiglu: out = gate / (1 + exp(-gate)) * up over count elements
+ * (count % 4 == 0), fp32 or fp16 output.  qi_hip_swiglu_quantize_fp6: the
+ * same values [m, k] quantised into the fp6 layout (bit-identical to
+ * quantising qi_hip_swiglu's fp32 output); k % 256 == 0.
+ *
+ * Outputs agree with the reference formulas within a few fp32 ulps (the
+ * reduction order and the rsqrt / exp implementations are this library's). */
+int qi_hip_layer_norm_scale(const float *x, const float *scale, int scale_stride, void *out, int out_type, int rows,
+                            int width, int split, void *stream);
+int qi_hip_layer_norm_scale_quantize_fp6(const float *x, const float *scale, int scale_stride, int split,
+                                         void *row_stats, void *codes6, int m, int k, void *stream);
+int qi_hip_swiglu(const float *gate, const float *up, void *out, int out_type, unsigned long long count,
+                  void *stream);
+int qi_hip_swiglu_quantize_fp6(const float *gate, const float *up, void *codes6, int m, int k, void *stream);
+
 /* Device-side QIPACK quantiser (int4_pack.cplus:237-468 arithmetic, bit-exact):
  * w_half fp16 [n, k] -> QIPACK arrays.  scheme 5 = W4A16 affine (minimums
  * required), scheme 6 = W4A4 H256 symmetric (minimums ignored).  group must

@@ -197,3 +197,23 @@ def fnv1a(data: bytes, h: int = 14695981039346656037) -> int:
 
 def num_threads() -> int:
     return int(lib().qo_num_threads())
+
+
+def layer_norm_scale(x, scale, split=0) -> np.ndarray:
+    """The reference's LayerNorm with modulation scale in float64
+    (qwen_image_cuda/cuda/ops.cu:37-53): per row, mean, mean of squared
+    deviations (two passes), (x - mean) / sqrt(var + 1e-6) * (1 + s) with s =
+    scale[1] for rows < split, else scale[0].  float64 result."""
+    x = np.asarray(x, np.float64)
+    scale = np.asarray(scale, np.float64)
+    mean = x.mean(axis=1, keepdims=True)
+    var = ((x - mean) ** 2).mean(axis=1, keepdims=True)
+    rows = np.arange(x.shape[0])[:, None]
+    s = np.where(rows < split, scale[1][None, :], scale[0][None, :])
+    return (x - mean) / np.sqrt(var + 1e-6) * (1.0 + s)
+
+
+def swiglu(gate, up) -> np.ndarray:
+    """silu(gate) * up in float64 (qwen_image_cuda/cuda/ops.cu:134-139)."""
+    g = np.asarray(gate, np.float64)
+    return g / (1.0 + np.exp(-g)) * np.asarray(up, np.float64)

@@ -14,6 +14,8 @@
 // shuffles.  A row of any length is just more chunks, so there is no per-row
 // LDS limit, and the grid has m * k / 256 wavefronts to spread over the CUs.
 
+#include <type_traits>
+
 #include "qi_common.h"
 
 namespace qi {
@@ -85,6 +87,8 @@ __device__ __forceinline__ uint32_t e2m3_of(int q) {
 template <typename In>
 __device__ __forceinline__ void quantize_chunk(float (&v)[4], float *buf, int lane, int (&q)[4],
                                                uint16_t &scale_bits) {
+    // In = uint16_t: the values are fp16 inputs (see butterfly4); any other
+    // type: arbitrary fp32 values.
     constexpr bool HALF = !__is_same(In, uint16_t);  // see butterfly4
     butterfly4<HALF>(v[0], v[1], v[2], v[3]);  // stride 1: in registers
 #pragma unroll
@@ -199,9 +203,18 @@ __global__ __launch_bounds__(QUANT_WAVES * WAVE) void quantize_chunks_kernel(
 // workgroups over every block).  Wave w takes rows w * RPW .. + RPW - 1 and
 // issues all their loads first.  Rows past m quantise zeros; their codes are
 // written but never used.
-template <typename In, int RPW>
+// No producer: the quantiser reads its input as is.
+struct NoProducer {
+    static constexpr bool active = false;
+    __device__ void operator()(int, int, float (&)[4]) const {}
+};
+
+template <typename In, int RPW, typename Producer = NoProducer>
 __global__ __launch_bounds__(32 / RPW * WAVE) void quantize_fp6_strip_kernel(
-    const In *__restrict__ x, uint8_t *__restrict__ codes, uint16_t *__restrict__ scales, int m, int k) {
+    const In *__restrict__ x, uint8_t *__restrict__ codes, uint16_t *__restrict__ scales, int m, int k,
+    Producer produce = Producer{}) {
+    // With a producer the values are arbitrary fp32, whatever the input type.
+    using Vals = typename std::conditional<Producer::active, float, In>::type;
     constexpr int NWV = 32 / RPW;
     __shared__ float lds[NWV][256];
     __shared__ __attribute__((aligned(16))) uint32_t blocks[4 * FP6_BLOCK / 4];
@@ -217,6 +230,7 @@ __global__ __launch_bounds__(32 / RPW * WAVE) void quantize_fp6_strip_kernel(
         const int row = tile * 32 + wave * RPW + i;
         if (row < m) {
             load4<In>(x + static_cast<size_t>(row) * k + c * 256 + lane * 4, in[i]);
+            produce(row, c * 256 + lane * 4, in[i]);
         } else {
 #pragma unroll
             for (int j = 0; j < 4; ++j) in[i][j] = 0.f;
@@ -233,7 +247,7 @@ __global__ __launch_bounds__(32 / RPW * WAVE) void quantize_fp6_strip_kernel(
         float v[4] = {in[i][0], in[i][1], in[i][2], in[i][3]};
         int q[4];
         uint16_t scale_bits;
-        quantize_chunk<In>(v, buf, lane, q, scale_bits);
+        quantize_chunk<Vals>(v, buf, lane, q, scale_bits);
         const int r32 = wave * RPW + i;
         const uint32_t bits =
             e2m3_of(q[0]) | (e2m3_of(q[1]) << 6) | (e2m3_of(q[2]) << 12) | (e2m3_of(q[3]) << 18);
@@ -271,6 +285,24 @@ __global__ void f32_to_f16_kernel(const float *__restrict__ src, uint16_t *__res
     }
 }
 
+// Grid: x = 32-row tile, y = chunk.  Four rows per wave (8 waves per
+// workgroup) when there are rows enough to fill the chip, else two (16
+// waves).  Shapes and pointers are checked by the callers.
+template <typename In, typename Producer>
+static int launch_fp6_strip(const In *x, void *codes, void *scales, int m, int k, hipStream_t stream,
+                            Producer produce) {
+    const int chunks = k / 256;
+    if (chunks > 65535) return kInvalid;
+    const dim3 grid(static_cast<unsigned>((m + 31) / 32), static_cast<unsigned>(chunks));
+    if (m >= 1024)
+        quantize_fp6_strip_kernel<In, 4, Producer><<<grid, dim3(8 * WAVE), 0, stream>>>(
+            x, static_cast<uint8_t *>(codes), static_cast<uint16_t *>(scales), m, k, produce);
+    else
+        quantize_fp6_strip_kernel<In, 2, Producer><<<grid, dim3(16 * WAVE), 0, stream>>>(
+            x, static_cast<uint8_t *>(codes), static_cast<uint16_t *>(scales), m, k, produce);
+    return launch_status();
+}
+
 template <typename In, int FMT>
 static int launch_quantize(const In *x, void *codes, void *scales, int m, int k, hipStream_t stream) {
     // The fp6 layout carries the scales inside the code blocks; its separate
@@ -284,19 +316,7 @@ static int launch_quantize(const In *x, void *codes, void *scales, int m, int k,
         reinterpret_cast<uintptr_t>(scales) % 2 != 0)
         return kInvalid;
     const int chunks = k / 256;
-    if (FMT == 1) {
-        if (chunks > 65535) return kInvalid;
-        const dim3 grid(static_cast<unsigned>((m + 31) / 32), static_cast<unsigned>(chunks));
-        // Four rows per wave (8 waves per workgroup) when there are rows
-        // enough to fill the chip, else two (16 waves).
-        if (m >= 1024)
-            quantize_fp6_strip_kernel<In, 4><<<grid, dim3(8 * WAVE), 0, stream>>>(
-                x, static_cast<uint8_t *>(codes), static_cast<uint16_t *>(scales), m, k);
-        else
-            quantize_fp6_strip_kernel<In, 2><<<grid, dim3(16 * WAVE), 0, stream>>>(
-                x, static_cast<uint8_t *>(codes), static_cast<uint16_t *>(scales), m, k);
-        return launch_status();
-    }
+    if (FMT == 1) return launch_fp6_strip<In>(x, codes, scales, m, k, stream, NoProducer{});
     // Several chunks per wave when there are rows enough to fill the chip.
     if (m >= 1024) {
         constexpr int CPW = 4;
@@ -325,6 +345,146 @@ static int launch_f32_to_f16(const float *src, void *out, unsigned long long cou
         src, static_cast<uint16_t *>(out), count);
     return launch_status();
 }
+
+
+// ---------------------------------------------------------------------------
+// Producers fused with the quantiser.  The reference runs each as its own
+// kernel writing fp32 activations that the quantiser then reads back
+// (transformer.cplus:759-760, 808-813): the affine-free LayerNorm with
+// modulation scale (ops.cu:37-58) before q/k/v and the MLP, and SwiGLU
+// (ops.cu:134-143) before the MLP's down projection.  Here the quantiser
+// applies them to the values it loads, so the fp32 intermediate never goes
+// through HBM.  The plain producer kernels below use the same device
+// arithmetic, so quantising their output gives the fused codes bit for bit.
+// Neither reproduces the reference's own reduction order or its CUDA
+// rsqrtf / expf: their outputs agree with the formulas within a few fp32
+// ulps.
+
+constexpr float LN_EPSILON = 1e-6f;  // ops.cu:12
+
+__device__ __forceinline__ float wave_sum64(float v) {
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) v += __shfl_xor(v, s, 64);
+    return v;  // the same value in every lane (each pairwise sum is symmetric)
+}
+
+// Row statistics of ops.cu:40-50: mean, then the mean of squared deviations
+// (two passes), inverse = 1 / sqrt(variance + 1e-6), correctly rounded sqrt
+// and division.  One wave per row; lane l sums elements 4l + 256 i, i = 0,
+// 1, ... in order, then the wave adds the lanes.  k % 4 == 0.
+__device__ __forceinline__ float2 ln_row_stats(const float *__restrict__ row, int k, int lane) {
+    float s = 0.f;
+    for (int i = lane * 4; i < k; i += 256) {
+        const float4 t = *reinterpret_cast<const float4 *>(row + i);
+        s = ((s + t.x) + t.y + t.z) + t.w;
+    }
+    const float mean = wave_sum64(s) / static_cast<float>(k);
+    float sq = 0.f;
+    for (int i = lane * 4; i < k; i += 256) {
+        const float4 t = *reinterpret_cast<const float4 *>(row + i);
+        float d = t.x - mean;
+        sq = __builtin_fmaf(d, d, sq);
+        d = t.y - mean;
+        sq = __builtin_fmaf(d, d, sq);
+        d = t.z - mean;
+        sq = __builtin_fmaf(d, d, sq);
+        d = t.w - mean;
+        sq = __builtin_fmaf(d, d, sq);
+    }
+    const float var = wave_sum64(sq) / static_cast<float>(k);
+    return float2{mean, 1.0f / __builtin_sqrtf(var + LN_EPSILON)};
+}
+
+// ops.cu:52-53: (x - mean) * inverse * (1 + scale[i]), the scale row chosen
+// by row < split (row 1 of the modulation, the prefix) or not (row 0).
+__device__ __forceinline__ void ln_scale_apply(float2 st, const float *__restrict__ s, float (&v)[4]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = ((v[e] - st.x) * st.y) * (1.0f + s[e]);
+}
+
+struct LnScaleProducer {
+    static constexpr bool active = true;
+    const float2 *stats;
+    const float *scale;
+    int scale_stride, split;
+    __device__ void operator()(int row, int col, float (&v)[4]) const {
+        ln_scale_apply(stats[row], scale + (row < split ? scale_stride : 0) + col, v);
+    }
+};
+
+// ops.cu:134-139: silu(gate) * up = gate / (1 + exp(-gate)) * up.
+__device__ __forceinline__ float swiglu1(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
+struct SwigluProducer {  // the quantiser's input is the gate
+    static constexpr bool active = true;
+    const float *up;
+    int k;
+    __device__ void operator()(int row, int col, float (&v)[4]) const {
+        const float4 u = *reinterpret_cast<const float4 *>(up + static_cast<size_t>(row) * k + col);
+        v[0] = swiglu1(v[0], u.x);
+        v[1] = swiglu1(v[1], u.y);
+        v[2] = swiglu1(v[2], u.z);
+        v[3] = swiglu1(v[3], u.w);
+    }
+};
+
+// One wave per row: the row statistics into stats[row].
+__global__ __launch_bounds__(4 * WAVE) void ln_stats_kernel(const float *__restrict__ x, float2 *__restrict__ stats,
+                                                             int m, int k) {
+    const int lane = threadIdx.x & (WAVE - 1), row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= m) return;
+    const float2 st = ln_row_stats(x + static_cast<size_t>(row) * k, k, lane);
+    if (lane == 0) stats[row] = st;
+}
+
+// The plain LayerNorm-scale (qi_layer_norm_scale), one wave per row, fp32 or
+// fp16 (RNE) output.
+__global__ __launch_bounds__(4 * WAVE) void layer_norm_scale_kernel(const float *__restrict__ x,
+                                                                     const float *__restrict__ scale, int scale_stride,
+                                                                     int split, void *__restrict__ out, int out_type,
+                                                                     int m, int k) {
+    const int lane = threadIdx.x & (WAVE - 1), row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= m) return;
+    const float *src = x + static_cast<size_t>(row) * k;
+    const float2 st = ln_row_stats(src, k, lane);
+    const float *s = scale + (row < split ? scale_stride : 0);
+    for (int i = lane * 4; i < k; i += 256) {
+        const float4 t = *reinterpret_cast<const float4 *>(src + i);
+        float v[4] = {t.x, t.y, t.z, t.w};
+        ln_scale_apply(st, s + i, v);
+        const size_t o = static_cast<size_t>(row) * k + i;
+        if (out_type == QI_HIP_OUT_F16) {
+            uint2 h;
+            h.x = static_cast<uint32_t>(f2h(v[0])) | (static_cast<uint32_t>(f2h(v[1])) << 16);
+            h.y = static_cast<uint32_t>(f2h(v[2])) | (static_cast<uint32_t>(f2h(v[3])) << 16);
+            *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(out) + o) = h;
+        } else {
+            *reinterpret_cast<float4 *>(static_cast<float *>(out) + o) = float4{v[0], v[1], v[2], v[3]};
+        }
+    }
+}
+
+// The plain SwiGLU (qi_swiglu), four elements per thread, fp32 or fp16 out.
+__global__ void swiglu_kernel(const float *__restrict__ gate, const float *__restrict__ up, void *__restrict__ out,
+                              int out_type, unsigned long long count) {
+    const unsigned long long stride = static_cast<unsigned long long>(gridDim.x) * blockDim.x * 4;
+    for (unsigned long long i = (static_cast<unsigned long long>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+         i < count; i += stride) {
+        const float4 g = *reinterpret_cast<const float4 *>(gate + i);
+        const float4 u = *reinterpret_cast<const float4 *>(up + i);
+        const float v[4] = {swiglu1(g.x, u.x), swiglu1(g.y, u.y), swiglu1(g.z, u.z), swiglu1(g.w, u.w)};
+        if (out_type == QI_HIP_OUT_F16) {
+            uint2 h;
+            h.x = static_cast<uint32_t>(f2h(v[0])) | (static_cast<uint32_t>(f2h(v[1])) << 16);
+            h.y = static_cast<uint32_t>(f2h(v[2])) | (static_cast<uint32_t>(f2h(v[3])) << 16);
+            *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(out) + i) = h;
+        } else {
+            *reinterpret_cast<float4 *>(static_cast<float *>(out) + i) = float4{v[0], v[1], v[2], v[3]};
+        }
+    }
+}
+
+static bool aligned16(const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
 }  // namespace qi
 
@@ -360,4 +520,56 @@ QI_API int qi_f32_to_f16(const float *source, void *out, unsigned long long coun
 
 QI_API int qi_hip_f32_to_f16(const float *source, void *out, unsigned long long count, void *stream) {
     return qi::launch_f32_to_f16(source, out, count, qi::stream_of(stream));
+}
+
+QI_API int qi_hip_layer_norm_scale(const float *x, const float *scale, int scale_stride, void *out, int out_type,
+                                   int rows, int width, int split, void *stream) {
+    using namespace qi;
+    if (rows < 0 || width <= 0 || width % 4 || scale_stride < 0) return kInvalid;
+    if (out_type != QI_HIP_OUT_F32 && out_type != QI_HIP_OUT_F16) return kInvalid;
+    if (rows == 0) return 0;
+    if (!x || !scale || !out || !aligned16(x) || !aligned16(out) || !aligned16(scale) || scale_stride % 4)
+        return kInvalid;
+    layer_norm_scale_kernel<<<dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(4 * WAVE), 0, stream_of(stream)>>>(
+        x, scale, scale_stride, split, out, out_type, rows, width);
+    return launch_status();
+}
+
+QI_API int qi_hip_layer_norm_scale_quantize_fp6(const float *x, const float *scale, int scale_stride, int split,
+                                                void *row_stats, void *codes6, int m, int k, void *stream) {
+    using namespace qi;
+    if (m < 0 || k <= 0 || k % 256 || scale_stride < 0) return kInvalid;
+    if (m == 0) return 0;
+    if (!x || !scale || !row_stats || !codes6 || !aligned16(x) || !aligned16(scale) || scale_stride % 4 ||
+        !aligned16(codes6) || reinterpret_cast<uintptr_t>(row_stats) % 8)
+        return kInvalid;
+    hipStream_t s = stream_of(stream);
+    ln_stats_kernel<<<dim3(static_cast<unsigned>((m + 3) / 4)), dim3(4 * WAVE), 0, s>>>(
+        x, static_cast<float2 *>(row_stats), m, k);
+    const int st = launch_status();
+    if (st) return st;
+    return launch_fp6_strip<float>(x, codes6, nullptr, m, k, s,
+                                   LnScaleProducer{static_cast<const float2 *>(row_stats), scale, scale_stride, split});
+}
+
+QI_API int qi_hip_swiglu(const float *gate, const float *up, void *out, int out_type, unsigned long long count,
+                         void *stream) {
+    using namespace qi;
+    if (count == 0) return 0;
+    if (count % 4 || out_type < 0 || out_type > 1 || !gate || !up || !out || !aligned16(gate) || !aligned16(up) ||
+        !aligned16(out))
+        return kInvalid;
+    unsigned long long blocks = (count / 4 + 255) / 256;
+    if (blocks > 65536ull * 16) blocks = 65536ull * 16;
+    swiglu_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream_of(stream)>>>(gate, up, out, out_type,
+                                                                                            count);
+    return launch_status();
+}
+
+QI_API int qi_hip_swiglu_quantize_fp6(const float *gate, const float *up, void *codes6, int m, int k, void *stream) {
+    using namespace qi;
+    if (m < 0 || k <= 0 || k % 256) return kInvalid;
+    if (m == 0) return 0;
+    if (!gate || !up || !codes6 || !aligned16(gate) || !aligned16(up) || !aligned16(codes6)) return kInvalid;
+    return launch_fp6_strip<float>(gate, codes6, nullptr, m, k, stream_of(stream), SwigluProducer{up, k});
 }

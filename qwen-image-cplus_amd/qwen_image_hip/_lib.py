@@ -38,6 +38,10 @@ SIGNATURES: dict[str, list] = {
     "qi_hip_w4a4_gemm_fp6": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
     "qi_hip_w4a4_gemm_fp6_parts": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p],
     "qi_hip_w4a16_gemm_tiled_parts": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p],
+    "qi_hip_layer_norm_scale": [_p, _p, _i, _p, _i, _i, _i, _i, _p],
+    "qi_hip_layer_norm_scale_quantize_fp6": [_p, _p, _i, _i, _p, _p, _i, _i, _p],
+    "qi_hip_swiglu": [_p, _p, _p, _i, _u64, _p],
+    "qi_hip_swiglu_quantize_fp6": [_p, _p, _p, _i, _i, _p],
     # QIPACK1 container (host I/O; QI_PACK_* status codes, not hipError_t).
     "qi_pack_open": [ctypes.c_char_p, _p],
     "qi_pack_info": [_p, _p, _p, _p, _p],

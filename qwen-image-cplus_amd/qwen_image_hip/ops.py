@@ -258,3 +258,54 @@ def w4a4_gemm_fp6(a_codes6, w_codes6, m: int, bias=None, out_dtype=torch.float32
                                            n if n_part is None else n_part, _stream())
     check(st, "w4a4 gemm")
     return y
+
+
+# ------------------------------------------------- producers + quantiser --
+
+
+def layer_norm_scale(x: torch.Tensor, scale: torch.Tensor, split: int = 0, out_dtype=torch.float32,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """The reference's LayerNorm with modulation scale (ops.cu:37-59) on fp32
+    x [rows, width]; scale is fp32 [2, width] (row 1 for rows < split)."""
+    rows, width = x.shape
+    if x.dtype != torch.float32 or scale.dtype != torch.float32 or scale.shape != (2, width):
+        raise ValueError("x fp32 [rows, width] and scale fp32 [2, width]")
+    out = out if out is not None else _empty((rows, width), out_dtype, x)
+    out_type = OUT_F16 if out.dtype == torch.float16 else OUT_F32
+    check(load().qi_hip_layer_norm_scale(_ptr(x), _ptr(scale), width, _ptr(out), out_type, rows, width, split,
+                                         _stream()), "layer norm")
+    return out
+
+
+def layer_norm_scale_quantize_fp6(x: torch.Tensor, scale: torch.Tensor, split: int = 0,
+                                  codes6: torch.Tensor | None = None, row_stats: torch.Tensor | None = None):
+    """layer_norm_scale fused with quantize_activations_fp6: codes only."""
+    m, k = x.shape
+    if x.dtype != torch.float32 or scale.dtype != torch.float32 or scale.shape != (2, k):
+        raise ValueError("x fp32 [m, k] and scale fp32 [2, k]")
+    codes6 = codes6 if codes6 is not None else _empty((fp6_rows(m), fp6_row_bytes(k)), torch.uint8, x)
+    row_stats = row_stats if row_stats is not None else _empty((m, 2), torch.float32, x)
+    check(load().qi_hip_layer_norm_scale_quantize_fp6(_ptr(x), _ptr(scale), k, split, _ptr(row_stats),
+                                                      _ptr(codes6), m, k, _stream()), "layer norm quantization")
+    return codes6
+
+
+def swiglu(gate: torch.Tensor, up: torch.Tensor, out_dtype=torch.float32, out: torch.Tensor | None = None):
+    """silu(gate) * up on fp32 tensors (ops.cu:134-144)."""
+    if gate.dtype != torch.float32 or up.shape != gate.shape or up.dtype != torch.float32:
+        raise ValueError("gate and up: fp32 tensors of one shape")
+    out = out if out is not None else _empty(gate.shape, out_dtype, gate)
+    out_type = OUT_F16 if out.dtype == torch.float16 else OUT_F32
+    check(load().qi_hip_swiglu(_ptr(gate), _ptr(up), _ptr(out), out_type, gate.numel(), _stream()), "swiglu")
+    return out
+
+
+def swiglu_quantize_fp6(gate: torch.Tensor, up: torch.Tensor, codes6: torch.Tensor | None = None):
+    """swiglu fused with quantize_activations_fp6: codes only."""
+    m, k = gate.shape
+    if gate.dtype != torch.float32 or up.shape != gate.shape or up.dtype != torch.float32:
+        raise ValueError("gate and up: fp32 tensors of one shape")
+    codes6 = codes6 if codes6 is not None else _empty((fp6_rows(m), fp6_row_bytes(k)), torch.uint8, gate)
+    check(load().qi_hip_swiglu_quantize_fp6(_ptr(gate), _ptr(up), _ptr(codes6), m, k, _stream()),
+          "swiglu quantization")
+    return codes6

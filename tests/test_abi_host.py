@@ -73,6 +73,14 @@ def test_extension_argument_checks():
     assert L.qi_hip_w4a4_gemm_fp6_parts(16, 16, None, 16, 0, 0, 4, 96, 256, 0, None) == INVALID
     assert L.qi_hip_w4a16_gemm_tiled_parts(16, 8, 8, None, 8, 0, 0, 5, 96, 64, 24, None) == INVALID
     assert L.qi_hip_w4a16_gemm_tiled_parts(16, 8, 8, None, 8, 0, 0, 5, 96, 64, 64, None) == INVALID
+    # producers: widths, alignment, output types, scratch
+    assert L.qi_hip_layer_norm_scale(16, 16, 16, 16, 0, 4, 30, 0, None) == INVALID          # width % 4
+    assert L.qi_hip_layer_norm_scale(16, 16, 16, 16, 2, 4, 32, 0, None) == INVALID          # out type
+    assert L.qi_hip_layer_norm_scale(16, 16, 16, 24, 0, 4, 32, 0, None) == INVALID          # out alignment
+    assert L.qi_hip_layer_norm_scale_quantize_fp6(16, 16, 256, 0, 16, 16, 4, 320, None) == INVALID  # k % 256
+    assert L.qi_hip_layer_norm_scale_quantize_fp6(16, 16, 256, 0, None, 16, 4, 256, None) == INVALID
+    assert L.qi_hip_swiglu(16, 16, 16, 0, 6, None) == INVALID                               # count % 4
+    assert L.qi_hip_swiglu_quantize_fp6(16, 16, 16, 4, 128, None) == INVALID               # k % 256
     # null pointers
     assert L.qi_w4a4_gemm(None, None, None, None, None, 128, 128, 256) == INVALID
 

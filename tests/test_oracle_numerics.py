@@ -340,3 +340,36 @@ def test_gelu_tanh_formula():
     v = np.linspace(-6, 6, 101).astype(np.float32)
     want = 0.5 * v.astype(np.float64) * (1 + np.tanh(np.sqrt(2 / np.pi) * (v + 0.044715 * v.astype(np.float64) ** 3)))
     np.testing.assert_allclose(oracle.gelu_tanh(v), want, rtol=1e-5, atol=1e-6)
+
+
+# ------------------------------------------- producers (LayerNorm, SwiGLU) --
+
+def test_layer_norm_scale_oracle_closed_forms():
+    import statistics
+    rng = np.random.default_rng(11)
+    x = rng.normal(3.0, 2.0, size=(6, 512))
+    zero = np.zeros((2, 512))
+    out = oracle.layer_norm_scale(x, zero)
+    # zero scale: each row has mean 0 and population variance var / (var + eps)
+    var = x.var(axis=1)
+    np.testing.assert_allclose(out.mean(axis=1), 0.0, atol=1e-12)
+    np.testing.assert_allclose(out.var(axis=1), var / (var + 1e-6), rtol=1e-12)
+    # shift invariance, and one row against the statistics module
+    np.testing.assert_allclose(oracle.layer_norm_scale(x + 100.0, zero), out, atol=1e-9)
+    row = list(x[2])
+    mu, pv = statistics.fmean(row), statistics.pvariance(row)
+    np.testing.assert_allclose(out[2], [(v - mu) / (pv + 1e-6) ** 0.5 for v in row], rtol=1e-12)
+    # the scale row: row 1 for rows < split, row 0 after; (1 + s) multiplies
+    scale = np.stack([np.full(512, 0.5), np.full(512, -0.25)])
+    got = oracle.layer_norm_scale(x, scale, split=2)
+    np.testing.assert_allclose(got[:2], out[:2] * 0.75, rtol=1e-12)
+    np.testing.assert_allclose(got[2:], out[2:] * 1.5, rtol=1e-12)
+
+
+def test_swiglu_oracle_known_values():
+    from scipy.special import expit
+    g = np.array([0.0, 1.0, -1.0, 30.0, -30.0, 2.5])
+    u = np.array([3.0, 2.0, 2.0, 1.0, 1.0, -4.0])
+    np.testing.assert_allclose(oracle.swiglu(g, u), g * expit(g) * u, rtol=1e-14)
+    assert oracle.swiglu(np.array([0.0]), np.array([5.0]))[0] == 0.0
+    np.testing.assert_allclose(oracle.swiglu(np.array([40.0]), np.array([1.0])), [40.0], rtol=1e-15)
