@@ -364,6 +364,40 @@ def bench_producers(iters=50):
     return out
 
 
+ENCODER_ROWS = 300  # config 4: prompt tokens through the Qwen2.5-VL-7B-shaped text encoder
+ENCODER_SHAPES = [("q", 3584, 3584), ("k+v fused", 2 * 512, 3584), ("gate+up fused", 2 * 18944, 3584),
+                  ("down", 3584, 18944)]
+
+
+def bench_encoder(iters=30):
+    """Config 4's encoder linears, W4A16 g64 at M=300 (k and v, gate and up as
+    fused records: one input each), fp16 in / fp16 out; per linear us and the
+    total fp16 TFLOP/s."""
+    import torch
+    import qwen_image_hip as q
+    from qwen_image_hip import ops
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(300)
+    x = {k: torch.randn((ENCODER_ROWS, k), generator=g, device="cuda").half() for k in (3584, 18944)}
+    out, total_ms, flops = {}, 0.0, 0.0
+    for name, n, k in ENCODER_SHAPES:
+        w = (torch.randn((n, k), generator=g, device="cuda") * 0.02).half()
+        rec = q.PackedLinear.from_fp16(q.SCHEME_W4A16, w)
+        del w
+        y = torch.empty((ENCODER_ROWS, n), dtype=torch.float16, device="cuda")
+        ms = time_fn(lambda: ops.w4a16_gemm(x[k], rec.tiled_codes, rec.tiled_scales,  # noqa: B023
+                                            out_dtype=torch.float16, y=y), iters, 5)
+        f = 2.0 * ENCODER_ROWS * n * k
+        out[name] = {"n": n, "k": k, "us": round(ms * 1e3, 2), "TFLOP_s": round(f / (ms * 1e-3) / 1e12, 1)}
+        total_ms += ms
+        flops += f
+        del rec
+    out["total"] = {"us": round(total_ms * 1e3, 2), "TFLOP_s": round(flops / (total_ms * 1e-3) / 1e12, 1),
+                    "frac_fp16_peak": round(flops / (total_ms * 1e-3) / PEAK_FP16_FLOPS, 4)}
+    return out
+
+
 STACK_STREAMS = {"image": 3 * 4096, "text": 512}  # config 5: 1024^2 edit with 2 reference images
 STACK_BLOCKS = 60
 
@@ -592,6 +626,8 @@ def main(argv=None) -> int:
         log(f"gemv: {extra['modulation_gemv']}")
         extra["producers"] = bench_producers()
         log(f"producers: {extra['producers']}")
+        extra["encoder_w4a16_m300"] = bench_encoder()
+        log(f"encoder: {extra['encoder_w4a16_m300']}")
         if not args.no_stack:
             log("packing the 60-block stack (config 5)")
             extra["stack60_w4a4"] = bench_stack()

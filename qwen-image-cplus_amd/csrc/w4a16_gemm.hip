@@ -16,6 +16,8 @@
 // double-buffered so one barrier per group suffices, and the next group's
 // codes, scales and activations are loaded while the current group computes.
 
+#include <cstdlib>
+
 #include "qi_common.h"
 
 namespace qi {
@@ -633,6 +635,24 @@ QI_API int qi_hip_w4a16_gemm_tiled_parts(const void *x_half, const void *w_tiled
     // workgroup's waves instead (measured on MI355X: 256 x 3072 x 3072 20.4
     // -> 17.5 us, 256 x 3072 x 12288 67.4 -> 49.3 us; wider N keeps the tiled
     // kernel).
+    // QI_HIP_W4A16_TILES forces a shape, for tuning: 1 K-split 64 x 64, 2
+    // tiled 32 x 64, 3 tiled 64 x 64, 4 tiled 128 x 192.
+    static const int forced = [] {
+        const char *e = getenv("QI_HIP_W4A16_TILES");
+        return e ? atoi(e) : -1;
+    }();
+    if (forced == 1)
+        return launch_splitk<4, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k, n_part,
+                                   stream_of(stream));
+    if (forced == 2)
+        return launch_tiled<2, 1, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
+                                     n_part, stream_of(stream));
+    if (forced == 3)
+        return launch_tiled<4, 1, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
+                                     n_part, stream_of(stream));
+    if (forced == 4 && n % 192 == 0)
+        return launch_tiled<8, 3, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
+                                     n_part, stream_of(stream));
     if (m <= 256 && static_cast<long long>((m + 31) / 32) * ((n + 63) / 64) < 1024)
         return launch_splitk<4, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k, n_part,
                                    stream_of(stream));
