@@ -35,7 +35,7 @@ PEAK_FP16_FLOPS = 2.5e15    # MI355X dense fp16 MFMA
 PEAK_HBM = 8.0e12           # MI355X HBM3E bytes/s
 TRAFFIC_FILE = ROOT / "profiles" / "w4a4_gemm_traffic.json"
 # The roofline kernel: its traffic record counts only when measured on it.
-DOMINANT_WORKLOAD = "w4a4 fp6 GEMM M=4096 N=9216 K=3072 (fused qkv), fp16 out"
+DOMINANT_WORKLOAD = "w4a4 fp6 dual-stream GEMM M=4096+256 N=9216 per stream K=3072 (fused qkv), fp16 out"
 
 
 def log(*a):
@@ -76,6 +76,12 @@ class Block:
             if operand == "fp6" or scheme == q.SCHEME_W4A16:
                 self.layers[(stream, "qkv")] = q.PackedLinear.fuse(
                     [self.layers[(stream, name)] for name in ("to_q", "to_k", "to_v")])
+        # fp6 W4A4: each linear's image and text records as one dual-stream
+        # record (both streams in one launch over their stacked rows).
+        if scheme == q.SCHEME_W4A4_H256 and operand == "fp6":
+            for name in ("qkv", "to_out", "mlp_up", "mlp_down"):
+                self.layers[("dual", name)] = q.PackedLinear.dual(
+                    [self.layers[(stream, name)] for stream in STREAMS])
         torch.cuda.synchronize()
 
 
@@ -119,8 +125,11 @@ PHASES = ("qkv", "out", "mlp")
 
 class StepW4A4:
     """One block's W4A4 linears through the transformer::linear mirror: every
-    distinct input quantised once (K and V reuse Q's codes), MLP up with the
-    fused GELU, its fp16 output quantised again for MLP down."""
+    distinct input quantised once, MLP up with the fused GELU, its fp16
+    output quantised again for MLP down.  fp6 records: the image and text
+    streams' rows stacked (image first) and each linear run as one
+    dual-stream record (to_q/to_k/to_v fused), so a step is four quantiser
+    and four GEMM launches.  int8 records: per stream, K/V reusing Q's codes."""
 
     def __init__(self, block: Block, seed: int, one_stream: bool = True):
         import torch
@@ -131,6 +140,7 @@ class StepW4A4:
         g = torch.Generator(device="cuda")
         g.manual_seed(seed)
         self.block = block
+        self.dual = ("dual", "qkv") in block.layers
         self.bufs = {}
         for stream, m in STREAMS.items():
             self.bufs[stream] = {
@@ -141,16 +151,35 @@ class StepW4A4:
                 "qkv": torch.empty((3, m, HIDDEN), dtype=torch.float16, device="cuda"),
                 "h": torch.empty((m, MLP), dtype=torch.float16, device="cuda"),
             }
+        if self.dual:
+            m = sum(STREAMS.values())
+            b = {name: torch.cat([self.bufs[st][name] for st in STREAMS], 0)
+                 for name in ("x_qkv", "x_out", "x_mlp")}
+            b.update({"work": q.Work(m, MLP, "cuda"),
+                      "y": torch.empty((m, HIDDEN), dtype=torch.float16, device="cuda"),
+                      "qkv": torch.empty((3, m, HIDDEN), dtype=torch.float16, device="cuda"),
+                      "h": torch.empty((m, MLP), dtype=torch.float16, device="cuda")})
+            self.bufs["stacked"] = b
 
     def outputs(self):
-        """Copies of the buffers the step writes last (per stream: MLP hidden h, down output y)."""
-        return [self.bufs[st][name].clone() for st in STREAMS for name in ("h", "y")]
+        """Copies of the buffers the step writes last (MLP hidden h, down output y)."""
+        keys = ["stacked"] if self.dual else list(STREAMS)
+        return [self.bufs[st][name].clone() for st in keys for name in ("h", "y")]
 
     def __call__(self):
         import torch
 
         lin = self.q.linear
         f16 = torch.float16
+        if self.dual:
+            b, w = self.bufs["stacked"], self.bufs["stacked"]["work"]
+            L = lambda name: self.block.layers[("dual", name)]  # noqa: E731
+            split = STREAMS["image"]
+            lin(L("qkv"), w, b["x_qkv"], b["qkv"], out_dtype=f16, split_rows=split)
+            lin(L("to_out"), w, b["x_out"], b["y"], out_dtype=f16, split_rows=split)
+            lin(L("mlp_up"), w, b["x_mlp"], b["h"], out_dtype=f16, gelu=True, split_rows=split)
+            lin(L("mlp_down"), w, b["h"], b["y"], out_dtype=f16, split_rows=split)
+            return
 
         def run_phase(stream, phase):
             b = self.bufs[stream]
@@ -230,49 +259,54 @@ def time_fn(fn, iters, warmup):
 
 
 def dominant_kernel(block: Block, step: StepW4A4):
-    """The image stream's fused to_q/to_k/to_v W4A4 GEMM (M=4096, N=3x3072,
-    K=3072; the step's largest launch besides MLP up), timed alone with HIP
-    events on the stream it is launched on."""
+    """The step's largest launch, the dual-stream fused QKV W4A4 GEMM (image
+    M=4096 and text M=256 rows stacked, N=3x3072 per stream, K=3072), timed
+    alone with HIP events on the stream it is launched on."""
     import torch
 
-    m = STREAMS["image"]
-    b = step.bufs["image"]
-    L = block.layers[("image", "qkv")]
+    b = step.bufs["stacked"]
+    L = block.layers[("dual", "qkv")]
     lin = step.q.linear
-    lin(L, b["work"], b["x_qkv"], b["qkv"], out_dtype=torch.float16)
-    fn = lambda: lin(L, b["work"], b["x_qkv"], b["qkv"], reuse_input=True, out_dtype=torch.float16)  # noqa: E731
+    split = STREAMS["image"]
+    lin(L, b["work"], b["x_qkv"], b["qkv"], out_dtype=torch.float16, split_rows=split)
+    fn = lambda: lin(L, b["work"], b["x_qkv"], b["qkv"], reuse_input=True, out_dtype=torch.float16,  # noqa: E731
+                     split_rows=split)
     ms = time_fn(fn, 50, 5)
-    ops_per_launch = 2.0 * m * (3 * HIDDEN) * HIDDEN
+    ops_per_launch = 2.0 * sum(STREAMS.values()) * (3 * HIDDEN) * HIDDEN
     return ms, ops_per_launch
 
 
 def kernel_only():
-    """The dominant W4A4 GEMM (fused QKV, 4096 x 9216 x 3072) x 20, then a
-    plain 512 MiB copy x 5 whose known byte count calibrates the FETCH_SIZE /
-    WRITE_SIZE counters."""
+    """The dominant W4A4 GEMM (dual-stream fused QKV, 4096 + 256 rows x 2 x 9216
+    x 3072) x 20, then a plain 512 MiB copy x 5 whose known byte count
+    calibrates the FETCH_SIZE / WRITE_SIZE counters."""
     import torch
     import qwen_image_hip as q
 
-    m = STREAMS["image"]
     g = torch.Generator(device="cuda")
     g.manual_seed(1)
-    recs = []
-    for _ in range(3):
-        w = (torch.randn((HIDDEN, HIDDEN), generator=g, device="cuda") * 0.02).half()
-        recs.append(q.PackedLinear.from_fp16(q.SCHEME_W4A4_H256, w, clip=True))
-    rec = q.PackedLinear.fuse(recs)
+    pairs = []
+    for _ in STREAMS:
+        recs = []
+        for _ in range(3):
+            w = (torch.randn((HIDDEN, HIDDEN), generator=g, device="cuda") * 0.02).half()
+            recs.append(q.PackedLinear.from_fp16(q.SCHEME_W4A4_H256, w, clip=True))
+        pairs.append(q.PackedLinear.fuse(recs))
+    rec = q.PackedLinear.dual(pairs)
+    m = sum(STREAMS.values())
     work = q.Work(m, HIDDEN, "cuda")
     x = heavy_tailed(m, HIDDEN, g)
     y = torch.empty((3, m, HIDDEN), dtype=torch.float16, device="cuda")
-    q.linear(rec, work, x, y, out_dtype=torch.float16)
+    split = STREAMS["image"]
+    q.linear(rec, work, x, y, out_dtype=torch.float16, split_rows=split)
     for _ in range(20):
-        q.linear(rec, work, x, y, reuse_input=True, out_dtype=torch.float16)
+        q.linear(rec, work, x, y, reuse_input=True, out_dtype=torch.float16, split_rows=split)
     src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda").fill_(1)
     dst = torch.empty_like(src)
     for _ in range(5):
         dst.copy_(src)
     torch.cuda.synchronize()
-    log("kernel-only: 20 x w4a4 GEMM 4096x9216x3072 (fused qkv), 5 x copy 536870912 B")
+    log("kernel-only: 20 x dual-stream w4a4 GEMM (4096+256)x(2x9216)x3072 (fused qkv), 5 x copy 536870912 B")
     return 0
 
 
@@ -406,10 +440,11 @@ def bench_stack(blocks=STACK_BLOCKS, steps=4):
     """Config 5: the full 60-block MMDiT linear stack, W4A4 H256 g64, image
     stream M=12288 + text stream M=512, every block with its own random-init
     weights packed by the device QIPACK quantiser (fp6 operand records, Q/K/V
-    fused), heavy-tailed fp16 activations quantised online before every
-    distinct input.  The block inputs are the same buffers in every block
-    (their values do not change the work).  One denoising step = the 60
-    blocks; `steps` steps are timed one by one with HIP events, the first
+    fused, each linear's two streams as one dual-stream record over the
+    stacked rows), heavy-tailed fp16 activations quantised online before
+    every distinct input.  The block inputs are the same buffers in every
+    block (their values do not change the work).  One denoising step = the
+    60 blocks; `steps` steps are timed one by one with HIP events, the first
     reported separately as the warm-up."""
     import torch
     import qwen_image_hip as q
@@ -418,7 +453,7 @@ def bench_stack(blocks=STACK_BLOCKS, steps=4):
     g.manual_seed(500)
     layers = []
     for _ in range(blocks):
-        blk = {}
+        per = {}
         for stream in STACK_STREAMS:
             qkv = []
             for name, n, k in block_shapes():
@@ -428,30 +463,29 @@ def bench_stack(blocks=STACK_BLOCKS, steps=4):
                 if name in ("to_q", "to_k", "to_v"):
                     qkv.append(rec)
                 else:
-                    blk[(stream, name)] = rec
-            blk[(stream, "qkv")] = q.PackedLinear.fuse(qkv)
+                    per[(stream, name)] = rec
+            per[(stream, "qkv")] = q.PackedLinear.fuse(qkv)
             del qkv
-        layers.append(blk)
-    bufs = {}
-    for stream, m in STACK_STREAMS.items():
-        bufs[stream] = {
-            "x_qkv": heavy_tailed(m, HIDDEN, g), "x_out": heavy_tailed(m, HIDDEN, g),
-            "x_mlp": heavy_tailed(m, HIDDEN, g), "work": q.Work(m, MLP, "cuda"),
-            "y": torch.empty((m, HIDDEN), dtype=torch.float16, device="cuda"),
-            "qkv": torch.empty((3, m, HIDDEN), dtype=torch.float16, device="cuda"),
-            "h": torch.empty((m, MLP), dtype=torch.float16, device="cuda"),
-        }
+        layers.append({name: q.PackedLinear.dual([per[(st, name)] for st in STACK_STREAMS])
+                       for name in ("qkv", "to_out", "mlp_up", "mlp_down")})
+        del per
+    m = sum(STACK_STREAMS.values())
+    split = STACK_STREAMS["image"]
+    b = {"x_qkv": heavy_tailed(m, HIDDEN, g), "x_out": heavy_tailed(m, HIDDEN, g),
+         "x_mlp": heavy_tailed(m, HIDDEN, g), "work": q.Work(m, MLP, "cuda"),
+         "y": torch.empty((m, HIDDEN), dtype=torch.float16, device="cuda"),
+         "qkv": torch.empty((3, m, HIDDEN), dtype=torch.float16, device="cuda"),
+         "h": torch.empty((m, MLP), dtype=torch.float16, device="cuda")}
     torch.cuda.synchronize()
     lin, f16 = q.linear, torch.float16
 
     def denoise_step():
+        w = b["work"]
         for blk in layers:
-            for stream in STACK_STREAMS:
-                b, w = bufs[stream], bufs[stream]["work"]
-                lin(blk[(stream, "qkv")], w, b["x_qkv"], b["qkv"], out_dtype=f16)
-                lin(blk[(stream, "to_out")], w, b["x_out"], b["y"], out_dtype=f16)
-                lin(blk[(stream, "mlp_up")], w, b["x_mlp"], b["h"], out_dtype=f16, gelu=True)
-                lin(blk[(stream, "mlp_down")], w, b["h"], b["y"], out_dtype=f16)
+            lin(blk["qkv"], w, b["x_qkv"], b["qkv"], out_dtype=f16, split_rows=split)
+            lin(blk["to_out"], w, b["x_out"], b["y"], out_dtype=f16, split_rows=split)
+            lin(blk["mlp_up"], w, b["x_mlp"], b["h"], out_dtype=f16, gelu=True, split_rows=split)
+            lin(blk["mlp_down"], w, b["h"], b["y"], out_dtype=f16, split_rows=split)
 
     times = []
     for _ in range(steps):
@@ -464,7 +498,7 @@ def bench_stack(blocks=STACK_BLOCKS, steps=4):
     ops_step = blocks * 2.0 * sum(n * k for _, n, k in block_shapes()) * sum(STACK_STREAMS.values())
     ms = sum(times[1:]) / max(1, len(times) - 1)
     tops = ops_step / (ms * 1e-3) / 1e12
-    del layers, bufs
+    del layers, b
     torch.cuda.empty_cache()
     return {"workload": f"config 5: {blocks}-block W4A4 stack, image M={STACK_STREAMS['image']} + text "
                         f"M={STACK_STREAMS['text']}", "ms_per_step": round(ms, 3),

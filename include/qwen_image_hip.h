@@ -177,6 +177,19 @@ int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *w_codes6, const float
  * output is bit-identical to the per-record call's. */
 int qi_hip_w4a4_gemm_fp6_parts(const void *a_codes6, const void *w_codes6, const float *bias, void *y,
                                int out_type, int epilogue, int m, int n, int k, int n_part, void *stream);
+/* Both streams of an MMDiT dual-stream block in one call (the reference
+ * runs the image and the text stream's linear as two
+ * transformer::linear calls on their own rows).  a_codes6: m rows of fp6
+ * activation blocks, rows [0, m_split) of stream 0 and [m_split, m) of
+ * stream 1 (one quantiser pass over the stacked rows); w_codes6: 2n weight
+ * rows, the first n stream 0's record, the next n stream 1's (each possibly
+ * a fused record with n / n_part parts); bias NULL or fp32 [2n].  y: n /
+ * n_part parts of [m, n_part], every row holding its own stream's outputs.
+ * Every output bit-identical to the per-stream calls.  0 < m_split < m,
+ * m_split % 32 == 0, n % 32 == 0, n_part as above.  One persistent launch
+ * when m, m_split and n are multiples of 128, else one launch per stream. */
+int qi_hip_w4a4_gemm_fp6_dual(const void *a_codes6, const void *w_codes6, const float *bias, void *y,
+                              int out_type, int epilogue, int m, int m_split, int n, int k, int n_part, void *stream);
 
 /* Producers fused with the activation quantiser.  The reference runs the
  * LayerNorm-with-modulation-scale (qi_layer_norm_scale, ops.cu:56-59) and

@@ -63,6 +63,15 @@ __device__ __forceinline__ v8i fp6_operand(v4i lo, v4i hi) {
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 4, 5, 6, -1, -1);
 }
 
+// Where outputs go.  Output (row, col) of the GEMM is element
+// (row_base + row, col - fold) of a y made of n_out / n_part parts of
+// [m_out, n_part] (out_index), where fold = n_out for the second stream's
+// columns (col >= n_out) of a dual-stream call and 0 otherwise.  A plain call
+// has row_base 0, m_out = m, n_out = n.
+struct Fp6Out {
+    int row_base, m_out, n_out;
+};
+
 template <int TM, int TN, int WM, int WN, int NSTAGE>
 struct Fp6Shape {
     static constexpr int MT = WM * TM, NTL = WN * TN;  // 32-row tiles of the block
@@ -81,7 +90,7 @@ template <int TM, int TN, int WM, int WN, int NSTAGE, bool WHOLE, typename Map>
 __device__ __forceinline__ void fp6_tiles(uint8_t *lds, const uint8_t *__restrict__ a6,
                                           const uint8_t *__restrict__ w6, const float *__restrict__ bias,
                                           void *__restrict__ y, int out_type, int epi, int m, int n, int k, int n_part,
-                                          int count, Map map) {
+                                          Fp6Out out, int count, Map map) {
     using S = Fp6Shape<TM, TN, WM, WN, NSTAGE>;
     constexpr int NW = WM * WN;
     constexpr int MT = S::MT, NTL = S::NTL;
@@ -245,13 +254,15 @@ __device__ __forceinline__ void fp6_tiles(uint8_t *lds, const uint8_t *__restric
             for (int j = 0; j < TN; ++j) {
                 const int tile_col = (nt0 + wn * TN + j) * 32;
                 if (tile_col >= n) continue;
+                const int fold = tile_col >= out.n_out ? out.n_out : 0;  // uniform
 #pragma unroll
                 for (int a = 0; a < 4; ++a) {
                     const int col = tile_col + 8 * a + 4 * (lane >> 5);
                     float v[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) v[r] = epilogue(acc[j][i][4 * a + r], bias, col + r, epi);
-                    const size_t idx = out_index(row, col, tile_col, m, n, n_part);
+                    const size_t idx =
+                        out_index(out.row_base + row, col - fold, tile_col - fold, out.m_out, out.n_out, n_part);
                     if (out_type == QI_HIP_OUT_F16) {
                         uint2 h;
                         h.x = static_cast<uint32_t>(f2h(v[0])) | (static_cast<uint32_t>(f2h(v[1])) << 16);
@@ -402,13 +413,13 @@ __device__ __forceinline__ void fp6_tiles(uint8_t *lds, const uint8_t *__restric
 template <int TM, int TN, int WM, int WN, int NSTAGE>
 __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2))) void w4a4_fp6_kernel(
     const uint8_t *__restrict__ a6, const uint8_t *__restrict__ w6, const float *__restrict__ bias,
-    void *__restrict__ y, int out_type, int epi, int m, int n, int k, int n_part) {
+    void *__restrict__ y, int out_type, int epi, int m, int n, int k, int n_part, Fp6Out out) {
     using S = Fp6Shape<TM, TN, WM, WN, NSTAGE>;
     __shared__ __attribute__((aligned(16))) uint8_t lds[S::LDS_BYTES];
     const int tiles_m = (m + S::BM - 1) / S::BM, tiles_n = (n + S::BN - 1) / S::BN;
     int tm, tn;
     tile_of_block(blockIdx.x, tiles_m, tiles_n, 8, tm, tn);
-    fp6_tiles<TM, TN, WM, WN, NSTAGE, false>(lds, a6, w6, bias, y, out_type, epi, m, n, k, n_part, 1,
+    fp6_tiles<TM, TN, WM, WN, NSTAGE, false>(lds, a6, w6, bias, y, out_type, epi, m, n, k, n_part, out, 1,
                                       [&](int, int &mt0, int &nt0) {
                                           mt0 = tm * S::MT;
                                           nt0 = tn * S::NTL;
@@ -427,33 +438,51 @@ __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2)
 // is computed once into LDS, outside the pipelined loop.
 constexpr int FP6_MAX_TILES = 128;
 
+// The 128 x 128 tile grid of a persistent call: t0 = tm0 * tn0 tiles of
+// stream 0 (tile rows from 0, tile columns from 0), then tm1 * tn1 tiles of
+// stream 1 (tile rows from tm0, columns from tn0) -- the two diagonal blocks
+// of a dual-stream call.  A plain call has tm1 = tn1 = 0.
+struct Fp6Grid {
+    int t0, tm0, tn0, tm1, tn1;
+};
+
+// 128 x 128 tile t of the grid, in XCD-aware order within each stream.
+__device__ __forceinline__ void grid_tile(const Fp6Grid &gd, int t, int &tm, int &tn) {
+    if (t < gd.t0) {
+        tile_of_block(t, gd.tm0, gd.tn0, 8, tm, tn);
+    } else {
+        tile_of_block(t - gd.t0, gd.tm1, gd.tn1, 8, tm, tn);
+        tm += gd.tm0;
+        tn += gd.tn0;
+    }
+}
+
 template <int TN, int WM, int WN, int NSTAGE>
 __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2))) void w4a4_fp6_persistent_kernel(
     const uint8_t *__restrict__ a6, const uint8_t *__restrict__ w6, const float *__restrict__ bias,
-    void *__restrict__ y, int out_type, int epi, int m, int n, int k, int n_part, int full_tiles,
-    int half_units) {
+    void *__restrict__ y, int out_type, int epi, int m, int n, int k, int n_part, Fp6Out out, Fp6Grid gd,
+    int full_tiles, int half_units) {
     static_assert(NSTAGE == 4, "tiles end on ring boundaries");
     using S2 = Fp6Shape<2, TN, WM, WN, NSTAGE>;
     using S1 = Fp6Shape<1, TN, WM, WN, NSTAGE>;
     static_assert(S2::LDS_BYTES >= S1::LDS_BYTES, "one LDS ring for both phases");
     __shared__ __attribute__((aligned(16))) uint8_t lds[S2::LDS_BYTES];
     __shared__ uint32_t tile_list[FP6_MAX_TILES];  // mt0 | nt0 << 16
-    const int tiles_m = (m + S2::BM - 1) / S2::BM, tiles_n = (n + S2::BN - 1) / S2::BN;
     const int b = blockIdx.x, stride = gridDim.x;
     const int count = b < full_tiles ? (full_tiles - 1 - b) / stride + 1 : 0;
     for (int j = threadIdx.x; j < count; j += blockDim.x) {
         int tm, tn;
-        tile_of_block(b + j * stride, tiles_m, tiles_n, 8, tm, tn);
+        grid_tile(gd, b + j * stride, tm, tn);
         tile_list[j] = static_cast<uint32_t>(tm * S2::MT) | (static_cast<uint32_t>(tn * S2::NTL) << 16);
     }
     __syncthreads();
     if (count > 0)
-        fp6_tiles<2, TN, WM, WN, NSTAGE, true>(lds, a6, w6, bias, y, out_type, epi, m, n, k, n_part, count,
-                                         [&](int j, int &mt0, int &nt0) {
-                                             const uint32_t e = __builtin_amdgcn_readfirstlane(tile_list[j]);
-                                             mt0 = static_cast<int>(e & 0xFFFFu);
-                                             nt0 = static_cast<int>(e >> 16);
-                                         });
+        fp6_tiles<2, TN, WM, WN, NSTAGE, true>(lds, a6, w6, bias, y, out_type, epi, m, n, k, n_part, out, count,
+                                               [&](int j, int &mt0, int &nt0) {
+                                                   const uint32_t e = __builtin_amdgcn_readfirstlane(tile_list[j]);
+                                                   mt0 = static_cast<int>(e & 0xFFFFu);
+                                                   nt0 = static_cast<int>(e >> 16);
+                                               });
     if (b < half_units) {
         // The ring is reused: every wave has finished with it (each wave's
         // own loads were drained at the end of the first phase).
@@ -467,23 +496,24 @@ __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2)
             half = b & 1;
         }
         int tm, tn;
-        tile_of_block(t, tiles_m, tiles_n, 8, tm, tn);
-        fp6_tiles<1, TN, WM, WN, NSTAGE, false>(lds, a6, w6, bias, y, out_type, epi, m, n, k, n_part, 1,
-                                         [&](int, int &mt0, int &nt0) {
-                                             mt0 = tm * S2::MT + half * S1::MT;
-                                             nt0 = tn * S1::NTL;
-                                         });
+        grid_tile(gd, t, tm, tn);
+        fp6_tiles<1, TN, WM, WN, NSTAGE, false>(lds, a6, w6, bias, y, out_type, epi, m, n, k, n_part, out, 1,
+                                                [&](int, int &mt0, int &nt0) {
+                                                    mt0 = tm * S2::MT + half * S1::MT;
+                                                    nt0 = tn * S1::NTL;
+                                                });
     }
 }
 
 template <int TM, int TN, int WM, int WN, int NSTAGE>
 static int launch_fp6(const void *a6, const void *w6, const float *bias, void *y,
-                      int out_type, int epi, int m, int n, int k, int n_part, hipStream_t stream) {
+                      int out_type, int epi, int m, int n, int k, int n_part, Fp6Out out, hipStream_t stream) {
     constexpr int BM = WM * TM * 32, BN = WN * TN * 32;
     const long long blocks = static_cast<long long>((m + BM - 1) / BM) * ((n + BN - 1) / BN);
     if (blocks > 0x7FFFFFFFLL) return kInvalid;
     w4a4_fp6_kernel<TM, TN, WM, WN, NSTAGE><<<dim3(static_cast<unsigned>(blocks)), dim3(WM * WN * WAVE), 0, stream>>>(
-        static_cast<const uint8_t *>(a6), static_cast<const uint8_t *>(w6), bias, y, out_type, epi, m, n, k, n_part);
+        static_cast<const uint8_t *>(a6), static_cast<const uint8_t *>(w6), bias, y, out_type, epi, m, n, k, n_part,
+        out);
     return launch_status();
 }
 
@@ -500,10 +530,19 @@ static int device_cus() {
     return cus[dev];
 }
 
-// 128 x 128 tiles, two workgroups per CU, persistent (see the kernel).
+// 128 x 128 tiles, two workgroups per CU, persistent (see the kernel); m,
+// n multiples of 128 (and for a dual call m_split and n_out too).  m_split
+// = 0: one stream.
 static int launch_fp6_persistent(const void *a6, const void *w6, const float *bias, void *y, int out_type, int epi,
-                                 int m, int n, int k, int n_part, hipStream_t stream) {
-    const long long tiles = static_cast<long long>((m + 127) / 128) * ((n + 127) / 128);
+                                 int m, int n, int k, int n_part, Fp6Out out, int m_split, hipStream_t stream) {
+    Fp6Grid gd;
+    if (m_split > 0) {
+        gd = Fp6Grid{(m_split / 128) * (out.n_out / 128), m_split / 128, out.n_out / 128, (m - m_split) / 128,
+                     (n - out.n_out) / 128};
+    } else {
+        gd = Fp6Grid{(m / 128) * (n / 128), m / 128, n / 128, 0, 0};
+    }
+    const long long tiles = static_cast<long long>(gd.t0) + static_cast<long long>(gd.tm1) * gd.tn1;
     const long long slots = 2LL * device_cus();
     long long full = tiles, halves = 0, grid;
     if (tiles >= slots) {
@@ -520,10 +559,11 @@ static int launch_fp6_persistent(const void *a6, const void *w6, const float *bi
     } else {
         grid = tiles;
     }
+    if (tiles <= 0) return 0;
     if (tiles > 0x7FFFFFFFLL || (full + grid - 1) / grid > FP6_MAX_TILES) return kInvalid;
     w4a4_fp6_persistent_kernel<2, 2, 2, 4><<<dim3(static_cast<unsigned>(grid)), dim3(4 * WAVE), 0, stream>>>(
         static_cast<const uint8_t *>(a6), static_cast<const uint8_t *>(w6), bias, y, out_type, epi, m, n, k, n_part,
-        static_cast<int>(full), static_cast<int>(halves));
+        out, gd, static_cast<int>(full), static_cast<int>(halves));
     return launch_status();
 }
 
@@ -531,21 +571,12 @@ static int launch_fp6_persistent(const void *a6, const void *w6, const float *bi
 
 using namespace qi;
 
-QI_API int qi_hip_w4a4_gemm_fp6_parts(const void *a_codes6, const void *w_codes6, const float *bias, void *y,
-                                      int out_type, int epilogue, int m, int n, int k, int n_part, void *stream) {
-    if (m <= 0 || n <= 0 || k <= 0 || n % 32 || k % 256) return kInvalid;
-    if (n_part <= 0 || n_part % 32 || n % n_part) return kInvalid;
-    if (!a_codes6 || !w_codes6 || !y) return kInvalid;
-    if (out_type != QI_HIP_OUT_F32 && out_type != QI_HIP_OUT_F16) return kInvalid;
-    if (epilogue != QI_HIP_EPILOGUE_NONE && epilogue != QI_HIP_EPILOGUE_GELU_TANH) return kInvalid;
-    if (reinterpret_cast<uintptr_t>(a_codes6) % 16 || reinterpret_cast<uintptr_t>(w_codes6) % 16 ||
-        reinterpret_cast<uintptr_t>(y) % (out_type == QI_HIP_OUT_F16 ? 8 : 16))
-        return kInvalid;
-    const long long g = k / 64;
-    if (static_cast<long long>((m + 31) / 32) * g * FP6_BLOCK >= (1LL << 31) ||
-        static_cast<long long>(n / 32) * g * FP6_BLOCK >= (1LL << 31))
-        return kInvalid;
-    hipStream_t s = stream_of(stream);
+namespace qi {
+
+// Tile-shape choice for one stream (see qi_hip_w4a4_gemm_fp6_parts); the
+// arguments are checked by the callers.
+static int dispatch_fp6(const void *a_codes6, const void *w_codes6, const float *bias, void *y, int out_type,
+                        int epilogue, int m, int n, int k, int n_part, Fp6Out out, hipStream_t s) {
     // Tile shapes (measured on MI355X): 128 x 128 with four waves when that
     // already gives two workgroups per CU (persistent when M and N are
     // multiples of 128); otherwise, for short M, single-
@@ -566,17 +597,72 @@ QI_API int qi_hip_w4a4_gemm_fp6_parts(const void *a_codes6, const void *w_codes6
     case 0:
         // The persistent kernel takes whole 128 x 128 tiles only.
         if (m % 128 == 0 && n % 128 == 0)
-            return launch_fp6_persistent(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, s);
-        return launch_fp6<2, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, s);
+            return launch_fp6_persistent(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, out, 0, s);
+        return launch_fp6<2, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, out, s);
     case 5:
-        return launch_fp6<2, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, s);
+        return launch_fp6<2, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, out, s);
     case 3:
-        return launch_fp6<1, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, s);
+        return launch_fp6<1, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, out, s);
     case 4:
-        return launch_fp6<1, 1, 1, 1, 8>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, s);
+        return launch_fp6<1, 1, 1, 1, 8>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, out, s);
     default:
-        return launch_fp6<2, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, s);
+        return launch_fp6<2, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, out, s);
     }
+}
+
+}  // namespace qi
+
+QI_API int qi_hip_w4a4_gemm_fp6_parts(const void *a_codes6, const void *w_codes6, const float *bias, void *y,
+                                      int out_type, int epilogue, int m, int n, int k, int n_part, void *stream) {
+    if (m <= 0 || n <= 0 || k <= 0 || n % 32 || k % 256) return kInvalid;
+    if (n_part <= 0 || n_part % 32 || n % n_part) return kInvalid;
+    if (!a_codes6 || !w_codes6 || !y) return kInvalid;
+    if (out_type != QI_HIP_OUT_F32 && out_type != QI_HIP_OUT_F16) return kInvalid;
+    if (epilogue != QI_HIP_EPILOGUE_NONE && epilogue != QI_HIP_EPILOGUE_GELU_TANH) return kInvalid;
+    if (reinterpret_cast<uintptr_t>(a_codes6) % 16 || reinterpret_cast<uintptr_t>(w_codes6) % 16 ||
+        reinterpret_cast<uintptr_t>(y) % (out_type == QI_HIP_OUT_F16 ? 8 : 16))
+        return kInvalid;
+    const long long g = k / 64;
+    if (static_cast<long long>((m + 31) / 32) * g * FP6_BLOCK >= (1LL << 31) ||
+        static_cast<long long>(n / 32) * g * FP6_BLOCK >= (1LL << 31))
+        return kInvalid;
+    return dispatch_fp6(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, Fp6Out{0, m, n},
+                        stream_of(stream));
+}
+
+QI_API int qi_hip_w4a4_gemm_fp6_dual(const void *a_codes6, const void *w_codes6, const float *bias, void *y,
+                                     int out_type, int epilogue, int m, int m_split, int n, int k, int n_part,
+                                     void *stream) {
+    if (m_split <= 0 || m_split >= m || m_split % 32) return kInvalid;
+    if (m <= 0 || n <= 0 || k <= 0 || n % 32 || k % 256) return kInvalid;
+    if (n_part <= 0 || n_part % 32 || n % n_part) return kInvalid;
+    if (!a_codes6 || !w_codes6 || !y) return kInvalid;
+    if (out_type != QI_HIP_OUT_F32 && out_type != QI_HIP_OUT_F16) return kInvalid;
+    if (epilogue != QI_HIP_EPILOGUE_NONE && epilogue != QI_HIP_EPILOGUE_GELU_TANH) return kInvalid;
+    if (reinterpret_cast<uintptr_t>(a_codes6) % 16 || reinterpret_cast<uintptr_t>(w_codes6) % 16 ||
+        reinterpret_cast<uintptr_t>(y) % (out_type == QI_HIP_OUT_F16 ? 8 : 16))
+        return kInvalid;
+    const long long g = k / 64;
+    if (static_cast<long long>((m + 31) / 32) * g * FP6_BLOCK >= (1LL << 31) ||
+        static_cast<long long>(2 * (n / 32)) * g * FP6_BLOCK >= (1LL << 31))
+        return kInvalid;
+    hipStream_t s = stream_of(stream);
+    static const int forced = [] {
+        const char *e = getenv("QI_HIP_FP6_TILES");
+        return e ? atoi(e) : -1;
+    }();
+    // Both streams in one persistent launch when every tile is whole.
+    if ((forced < 0 || forced == 0) && m % 128 == 0 && m_split % 128 == 0 && n % 128 == 0)
+        return launch_fp6_persistent(a_codes6, w_codes6, bias, y, out_type, epilogue, m, 2 * n, k, n_part,
+                                     Fp6Out{0, m, n}, m_split, s);
+    // Otherwise one launch per stream, each writing its rows of y.
+    const size_t gs = static_cast<size_t>(k / 64);
+    int st = dispatch_fp6(a_codes6, w_codes6, bias, y, out_type, epilogue, m_split, n, k, n_part, Fp6Out{0, m, n}, s);
+    if (st) return st;
+    return dispatch_fp6(static_cast<const uint8_t *>(a_codes6) + static_cast<size_t>(m_split / 32) * gs * FP6_BLOCK,
+                        static_cast<const uint8_t *>(w_codes6) + static_cast<size_t>(n / 32) * gs * FP6_BLOCK,
+                        bias ? bias + n : nullptr, y, out_type, epilogue, m - m_split, n, k, n_part,
+                        Fp6Out{m_split, m, n}, s);
 }
 
 QI_API int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *w_codes6, const float *bias, void *y,

@@ -52,6 +52,26 @@ class PackedLinear:
     bias: torch.Tensor | None = None  # fp32 [n] or None (the reference has none)
     operand: str = W4A4_FP6  # W4A4 records only
     parts: int = 1  # > 1: records fused along n (fuse()); outputs [parts, rows, n / parts]
+    streams: int = 1  # 2: a dual-stream pair (dual()); n is per stream
+
+    @classmethod
+    def dual(cls, records: "list[PackedLinear]") -> "PackedLinear":
+        """The image and text streams' records of one MMDiT block linear
+        (same shape), run by one call over the stacked rows of both streams
+        (``linear(..., split_rows=image_rows)``); fp6 W4A4 records only."""
+        if len(records) != 2:
+            raise ValueError("a dual-stream record pairs exactly two records")
+        a, b = records
+        if (a.scheme, a.n, a.k, a.operand, a.parts, a.streams) != (b.scheme, b.n, b.k, b.operand, b.parts, 1) \
+                or a.streams != 1:
+            raise ValueError("dual-stream records need one scheme, shape and operand format")
+        if a.scheme != SCHEME_W4A4_H256 or a.operand != W4A4_FP6:
+            raise ValueError("dual-stream records run on the fp6 W4A4 path")
+        if (a.bias is None) != (b.bias is None):
+            raise ValueError("either both records have a bias or neither has")
+        bias = None if a.bias is None else torch.cat([a.bias, b.bias], 0)
+        return cls(a.scheme, a.n, a.k, torch.cat([a.tiled_codes, b.tiled_codes], 0), None, bias, a.operand,
+                   a.parts, 2)
 
     @classmethod
     def fuse(cls, records: "list[PackedLinear]") -> "PackedLinear":
@@ -145,13 +165,15 @@ class Work:
 
 def linear(record: PackedLinear, work: Work, input: torch.Tensor, output: torch.Tensor | None = None,
            rows: int | None = None, reuse_input: bool = False, gelu: bool = False,
-           out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+           out_dtype: torch.dtype = torch.float32, split_rows: int | None = None) -> torch.Tensor:
     """output[rows, N] = input[rows, K] . W^T (+ bias, GELU) for one record.
 
     ``input`` is fp32 (the engine's activations) or fp16.  ``reuse_input``
     skips the quantisation / conversion when the previous linear already
     processed the same input (Q/K/V and gate/up in the reference).  A fused
     record (``PackedLinear.fuse``) writes ``output[parts, rows, N / parts]``.
+    A dual-stream record (``PackedLinear.dual``) takes the two streams' rows
+    stacked in ``input`` (the first ``split_rows`` rows are stream 0's).
     """
     n_part = record.n // record.parts if record.parts > 1 else None
     rows = input.shape[0] if rows is None else rows
@@ -163,6 +185,11 @@ def linear(record: PackedLinear, work: Work, input: torch.Tensor, output: torch.
         codes6 = work.fp6_views(rows, k)
         if not reuse_input:
             ops.quantize_activations_fp6(input[:rows], codes6)
+        if record.streams == 2:
+            if split_rows is None:
+                raise ValueError("a dual-stream record needs split_rows")
+            return ops.w4a4_gemm_fp6_dual(codes6, record.tiled_codes, rows, split_rows, record.bias, out_dtype, gelu,
+                                          output, n_part)
         return ops.w4a4_gemm_fp6(codes6, record.tiled_codes, rows, record.bias, out_dtype, gelu, output, n_part)
     if record.parts > 1 and record.scheme == SCHEME_W4A4_H256:
         raise ValueError("fused W4A4 records run on the fp6 operand format")

@@ -260,6 +260,22 @@ def w4a4_gemm_fp6(a_codes6, w_codes6, m: int, bias=None, out_dtype=torch.float32
     return y
 
 
+
+def w4a4_gemm_fp6_dual(a_codes6, w_codes6, m: int, m_split: int, bias=None, out_dtype=torch.float32, gelu=False,
+                       y=None, n_part=None):
+    """Both streams of a dual-stream block (qi_hip_w4a4_gemm_fp6_dual): rows
+    < m_split use the first half of w_codes6's rows, the others the second;
+    y is [m, n] (or [n / n_part, m, n_part]) with n = w_codes6 rows / 2."""
+    n2, k = w_codes6.shape[0], w_codes6.shape[1] // 56 * GROUP
+    n = n2 // 2
+    out_type = OUT_F16 if out_dtype == torch.float16 else OUT_F32
+    y = y if y is not None else _empty(_out_shape(m, n, n_part), out_dtype, w_codes6)
+    st = load().qi_hip_w4a4_gemm_fp6_dual(_ptr(a_codes6), _ptr(w_codes6), _ptr(bias), _ptr(y), out_type,
+                                          EPILOGUE_GELU_TANH if gelu else EPILOGUE_NONE, m, m_split, n, k,
+                                          n if n_part is None else n_part, _stream())
+    check(st, "w4a4 gemm")
+    return y
+
 # ------------------------------------------------- producers + quantiser --
 
 

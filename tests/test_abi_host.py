@@ -73,6 +73,10 @@ def test_extension_argument_checks():
     assert L.qi_hip_w4a4_gemm_fp6_parts(16, 16, None, 16, 0, 0, 4, 96, 256, 0, None) == INVALID
     assert L.qi_hip_w4a16_gemm_tiled_parts(16, 8, 8, None, 8, 0, 0, 5, 96, 64, 24, None) == INVALID
     assert L.qi_hip_w4a16_gemm_tiled_parts(16, 8, 8, None, 8, 0, 0, 5, 96, 64, 64, None) == INVALID
+    # dual-stream split must be inside (0, m) and on a 32-row tile
+    assert L.qi_hip_w4a4_gemm_fp6_dual(16, 16, None, 16, 0, 0, 256, 0, 64, 256, 64, None) == INVALID
+    assert L.qi_hip_w4a4_gemm_fp6_dual(16, 16, None, 16, 0, 0, 256, 256, 64, 256, 64, None) == INVALID
+    assert L.qi_hip_w4a4_gemm_fp6_dual(16, 16, None, 16, 0, 0, 256, 40, 64, 256, 64, None) == INVALID
     # producers: widths, alignment, output types, scratch
     assert L.qi_hip_layer_norm_scale(16, 16, 16, 16, 0, 4, 30, 0, None) == INVALID          # width % 4
     assert L.qi_hip_layer_norm_scale(16, 16, 16, 16, 2, 4, 32, 0, None) == INVALID          # out type

@@ -256,3 +256,38 @@ def test_fused_qkv_record_matches_separate_records(dev, m):
     for i, r in enumerate(recs):
         want = q.linear(r, work, x, reuse_input=True, out_dtype=torch.float16, gelu=True)
         torch.testing.assert_close(got[i], want, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("m_img,m_txt,fuse", [(4096, 256, True), (640, 128, False), (320, 37, True)])
+def test_dual_stream_record_matches_per_stream_calls(dev, m_img, m_txt, fuse):
+    """The image and text streams' linears as one dual-stream call on the
+    stacked rows: every output bit-identical to each stream's own call
+    (4096 + 256, 640 + 128: one persistent launch; 320 + 37: one launch per
+    stream)."""
+    import qwen_image_hip as q
+    n, k = 1024, 512
+    m = m_img + m_txt
+    print(f"fp6 dual stream m={m_img}+{m_txt} fuse={fuse}", flush=True)
+    x = _dev(heavy_tailed(m, k, 740 + m), dev)
+    bias = [_dev(np.random.default_rng(742 + s).normal(0, 0.5, size=(3 if fuse else 1) * n).astype(np.float32), dev)
+            for s in range(2)]
+    recs = []
+    for s in range(2):
+        parts = [q.PackedLinear.from_fp16(q.SCHEME_W4A4_H256,
+                                          _dev(weights_f16(n, k, 743 + 10 * s + i), dev).view(torch.float16),
+                                          clip=True) for i in range(3 if fuse else 1)]
+        r = q.PackedLinear.fuse(parts) if fuse else parts[0]
+        r.bias = bias[s]
+        recs.append(r)
+    pair = q.PackedLinear.dual(recs)
+    work = q.Work(m, k, dev)
+    got = q.linear(pair, work, x, out_dtype=torch.float16, gelu=True, split_rows=m_img)
+    w1 = q.Work(m_txt, k, dev)
+    want0 = q.linear(recs[0], work, x[:m_img], out_dtype=torch.float16, gelu=True)
+    want1 = q.linear(recs[1], w1, x[m_img:].contiguous(), out_dtype=torch.float16, gelu=True)
+    if fuse:
+        torch.testing.assert_close(got[:, :m_img], want0, rtol=0, atol=0)
+        torch.testing.assert_close(got[:, m_img:], want1, rtol=0, atol=0)
+    else:
+        torch.testing.assert_close(got[:m_img], want0, rtol=0, atol=0)
+        torch.testing.assert_close(got[m_img:], want1, rtol=0, atol=0)
