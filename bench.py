@@ -76,9 +76,10 @@ class Block:
             if operand == "fp6" or scheme == q.SCHEME_W4A16:
                 self.layers[(stream, "qkv")] = q.PackedLinear.fuse(
                     [self.layers[(stream, name)] for name in ("to_q", "to_k", "to_v")])
-        # fp6 W4A4: each linear's image and text records as one dual-stream
-        # record (both streams in one launch over their stacked rows).
-        if scheme == q.SCHEME_W4A4_H256 and operand == "fp6":
+        # fp6 W4A4 and W4A16: each linear's image and text records as one
+        # dual-stream record (both streams in one launch over their stacked
+        # rows).
+        if operand == "fp6" or scheme == q.SCHEME_W4A16:
             for name in ("qkv", "to_out", "mlp_up", "mlp_down"):
                 self.layers[("dual", name)] = q.PackedLinear.dual(
                     [self.layers[(stream, name)] for stream in STREAMS])
@@ -201,44 +202,38 @@ class StepW4A4:
 
 
 class StepW4A16:
+    """One block's W4A16 linears: the image and text streams' rows stacked
+    (image first), each linear one dual-stream record (to_q/to_k/to_v
+    fused), fp16 activations, MLP up with the fused GELU feeding MLP down."""
+
     def __init__(self, block: Block, seed: int, one_stream: bool = True):
         import torch
         from qwen_image_hip import ops
 
         self.ops = ops
-        self.side = None if one_stream else torch.cuda.Stream()
         g = torch.Generator(device="cuda")
         g.manual_seed(seed)
         self.block = block
-        self.bufs = {}
-        for stream, m in STREAMS.items():
-            self.bufs[stream] = {
-                "x": torch.randn((m, HIDDEN), generator=g, device="cuda").half(),
-                "y": torch.empty((m, HIDDEN), dtype=torch.float16, device="cuda"),
-                "qkv": torch.empty((3, m, HIDDEN), dtype=torch.float16, device="cuda"),
-                "h": torch.empty((m, MLP), dtype=torch.float16, device="cuda"),
-            }
+        m = sum(STREAMS.values())
+        self.b = {
+            "x": torch.randn((m, HIDDEN), generator=g, device="cuda").half(),
+            "y": torch.empty((m, HIDDEN), dtype=torch.float16, device="cuda"),
+            "qkv": torch.empty((3, m, HIDDEN), dtype=torch.float16, device="cuda"),
+            "h": torch.empty((m, MLP), dtype=torch.float16, device="cuda"),
+        }
 
     def __call__(self):
-        ops = self.ops
-
-        def run_phase(stream, phase):
-            b = self.bufs[stream]
-            L = lambda name: self.block.layers[(stream, name)]  # noqa: E731
-            if phase == "qkv":
-                r = L("qkv")
-                ops.w4a16_gemm(b["x"], r.tiled_codes, r.tiled_scales, out_dtype=ops.torch.float16, y=b["qkv"],
-                               n_part=HIDDEN)
-            if phase == "out":
-                r = L("to_out")
-                ops.w4a16_gemm(b["x"], r.tiled_codes, r.tiled_scales, out_dtype=ops.torch.float16, y=b["y"])
-            if phase == "mlp":
-                ops.w4a16_gemm(b["x"], L("mlp_up").tiled_codes, L("mlp_up").tiled_scales,
-                               out_dtype=ops.torch.float16, gelu=True, y=b["h"])
-                ops.w4a16_gemm(b["h"], L("mlp_down").tiled_codes, L("mlp_down").tiled_scales,
-                               out_dtype=ops.torch.float16, y=b["y"])
-
-        two_streams(run_phase, self.side)
+        ops, b, f16 = self.ops, self.b, self.ops.torch.float16
+        L = lambda name: self.block.layers[("dual", name)]  # noqa: E731
+        split = STREAMS["image"]
+        r = L("qkv")
+        ops.w4a16_gemm_dual(b["x"], r.tiled_codes, r.tiled_scales, split, out_dtype=f16, y=b["qkv"], n_part=HIDDEN)
+        r = L("to_out")
+        ops.w4a16_gemm_dual(b["x"], r.tiled_codes, r.tiled_scales, split, out_dtype=f16, y=b["y"])
+        r = L("mlp_up")
+        ops.w4a16_gemm_dual(b["x"], r.tiled_codes, r.tiled_scales, split, out_dtype=f16, gelu=True, y=b["h"])
+        r = L("mlp_down")
+        ops.w4a16_gemm_dual(b["h"], r.tiled_codes, r.tiled_scales, split, out_dtype=f16, y=b["y"])
 
 
 def time_fn(fn, iters, warmup):

@@ -136,6 +136,18 @@ int qi_hip_w4a16_gemm_tiled(const void *x_half, const void *w_tiled_codes, const
 int qi_hip_w4a16_gemm_tiled_parts(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
                                   const float *bias, void *y, int out_type, int epilogue, int m, int n, int k,
                                   int n_part, void *stream);
+/* Both streams of an MMDiT dual-stream block in one call (the W4A16 twin of
+ * qi_hip_w4a4_gemm_fp6_dual): x_half [m, k] holds stream 0's rows
+ * [0, m_split) then stream 1's; the tiled weight and scale arrays hold 2n
+ * rows, stream 0's record then stream 1's; bias NULL or fp32 [2n]; y is n /
+ * n_part parts of [m, n_part], each row with its own stream's outputs.  One
+ * launch over both streams' tiles when the kernel shape chosen for (m, n)
+ * tiles both blocks, else one launch per stream; outputs agree with the
+ * per-stream calls within the W4A16 tolerance.  Each stream has more than
+ * 16 rows. */
+int qi_hip_w4a16_gemm_tiled_dual(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
+                                 const float *bias, void *y, int out_type, int epilogue, int m, int m_split, int n,
+                                 int k, int n_part, void *stream);
 
 /* Bandwidth-bound W4A16 GEMV for 1 <= m <= 16 (the adaLN / timestep
  * modulation linears).  Same arithmetic and layouts as above.  The

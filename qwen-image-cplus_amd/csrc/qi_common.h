@@ -33,6 +33,21 @@ inline int launch_status() { return static_cast<int>(hipGetLastError()); }
 
 constexpr int kInvalid = static_cast<int>(hipErrorInvalidValue);
 
+// Compute units of the current device, read once per device.
+inline int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int c = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+        cus[dev] = c;
+    }
+    return cus[dev];
+}
+
+
+
 // fp16 bits <-> float on the device.  __builtin bit casts keep this exact.
 __device__ __forceinline__ float h2f(uint16_t bits) {
     _Float16 h = __builtin_bit_cast(_Float16, bits);
@@ -231,6 +246,34 @@ __device__ __forceinline__ void tile_of_block(int block, int tiles_m, int tiles_
     const int in_band = b % per_band;
     tm = first_m + in_band % rows;
     tn = in_band / rows;
+}
+
+// Where a GEMM's outputs go.  Output (row, col) is element
+// (row_base + row, col - fold) of a y made of n_out / n_part parts of
+// [m_out, n_part] (out_index), where fold = n_out for the second stream's
+// columns (col >= n_out) of a dual-stream call and 0 otherwise.  A plain
+// call has row_base 0, m_out = m, n_out = n.
+struct OutMap {
+    int row_base, m_out, n_out;
+};
+
+// The output-tile grid of a launch: t0 = tm0 * tn0 tiles of stream 0 (tile
+// rows and columns from 0), then tm1 * tn1 tiles of stream 1 (tile rows
+// from tm0, columns from tn0) -- the two diagonal blocks of a dual-stream
+// call.  A plain call has tm1 = tn1 = 0.
+struct TileGrid2 {
+    int t0, tm0, tn0, tm1, tn1;
+};
+
+// Tile t of the grid, in XCD-aware order within each stream.
+__device__ __forceinline__ void grid_tile(const TileGrid2 &gd, int t, int &tm, int &tn) {
+    if (t < gd.t0) {
+        tile_of_block(t, gd.tm0, gd.tn0, 8, tm, tn);
+    } else {
+        tile_of_block(t - gd.t0, gd.tm1, gd.tn1, 8, tm, tn);
+        tm += gd.tm0;
+        tn += gd.tn0;
+    }
 }
 
 // Epilogue store of one fp32 value.

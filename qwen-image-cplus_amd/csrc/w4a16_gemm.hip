@@ -288,7 +288,8 @@ __device__ __forceinline__ void w4a16_group_mfma(const uint8_t *xs, const v2i (&
 template <int TM, int TN, int NW>
 __global__ __launch_bounds__(NW *WAVE, (NW >= 8 ? 1 : 2)) void w4a16_tiled_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
-    const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int m, int n, int k, int n_part) {
+    const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int m, int n, int k, int n_part,
+    OutMap out, TileGrid2 gd) {
     constexpr int NSTAGE = 4;
     constexpr int BM = TM * 16, BN = NW * TN * 16;
     constexpr int A_INSTR = BM / 8;  // 1 KiB = 8 rows x 128 bytes per direct load
@@ -300,9 +301,8 @@ __global__ __launch_bounds__(NW *WAVE, (NW >= 8 ? 1 : 2)) void w4a16_tiled_kerne
     const int groups = k >> 6;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
     const int q = lane >> 4, r16 = lane & 15;
-    const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
     int tm, tn;
-    tile_of_block(blockIdx.x, tiles_m, tiles_n, 8, tm, tn);
+    grid_tile(gd, blockIdx.x, tm, tn);
     const int block_row = tm * BM, block_col = tn * BN;
 
     const uint32_t x_bytes = static_cast<uint32_t>(m) * static_cast<uint32_t>(k) * 2u;
@@ -387,6 +387,7 @@ __global__ __launch_bounds__(NW *WAVE, (NW >= 8 ? 1 : 2)) void w4a16_tiled_kerne
         const int col0 = block_col + (wave * TN + j) * 16;  // wave-uniform
         const int col = col0 + 4 * q;
         if (col >= n) continue;
+        const int fold = col0 >= out.n_out ? out.n_out : 0;
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             const int row = block_row + 16 * i + r16;
@@ -394,7 +395,7 @@ __global__ __launch_bounds__(NW *WAVE, (NW >= 8 ? 1 : 2)) void w4a16_tiled_kerne
             float v[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) v[r] = epilogue(acc[j][i][r], bias, col + r, epi);
-            const size_t idx = out_index(row, col, col0, m, n, n_part);
+            const size_t idx = out_index(out.row_base + row, col - fold, col0 - fold, out.m_out, out.n_out, n_part);
             if (out_type == QI_HIP_OUT_F16) {
                 uint2 h;
                 h.x = static_cast<uint32_t>(f2h(v[0])) | (static_cast<uint32_t>(f2h(v[1])) << 16);
@@ -409,13 +410,22 @@ __global__ __launch_bounds__(NW *WAVE, (NW >= 8 ? 1 : 2)) void w4a16_tiled_kerne
 
 template <int TM, int TN, int NW>
 static int launch_tiled(const void *x, const void *codes, const void *scales, const float *bias, void *y,
-                        int out_type, int epi, int m, int n, int k, int n_part, hipStream_t stream) {
+                        int out_type, int epi, int m, int n, int k, int n_part, OutMap out, int m_split,
+                        hipStream_t stream) {
     constexpr int BM = TM * 16, BN = NW * TN * 16;
-    const long long blocks = static_cast<long long>((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+    // One grid (m_split = 0), or the two streams' diagonal blocks (m_split
+    // and out.n_out multiples of BM and BN, checked by the caller).
+    TileGrid2 gd;
+    if (m_split > 0)
+        gd = TileGrid2{(m_split / BM) * (out.n_out / BN), m_split / BM, out.n_out / BN, (m - m_split + BM - 1) / BM,
+                       (n - out.n_out + BN - 1) / BN};
+    else
+        gd = TileGrid2{((m + BM - 1) / BM) * ((n + BN - 1) / BN), (m + BM - 1) / BM, (n + BN - 1) / BN, 0, 0};
+    const long long blocks = static_cast<long long>(gd.t0) + static_cast<long long>(gd.tm1) * gd.tn1;
     if (blocks > 0x7FFFFFFFLL) return kInvalid;
     w4a16_tiled_kernel<TM, TN, NW><<<dim3(static_cast<unsigned>(blocks)), dim3(NW * WAVE), 0, stream>>>(
         static_cast<const uint16_t *>(x), static_cast<const uint8_t *>(codes), static_cast<const uint16_t *>(scales),
-        bias, y, out_type, epi, m, n, k, n_part);
+        bias, y, out_type, epi, m, n, k, n_part, out, gd);
     return launch_status();
 }
 
@@ -432,7 +442,8 @@ static int launch_tiled(const void *x, const void *codes, const void *scales, co
 template <int TM, int TN>
 __global__ __launch_bounds__(4 * WAVE) void w4a16_splitk_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
-    const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int m, int n, int k, int n_part) {
+    const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int m, int n, int k, int n_part,
+    OutMap out) {
     constexpr int NW = 4, NSTAGE = 4;
     constexpr int BM = TM * 16, BN = TN * 16;
     constexpr int A_PER_W = BM / 8;  // 1 KiB direct loads: rows 8u .. 8u+7
@@ -539,7 +550,7 @@ __global__ __launch_bounds__(4 * WAVE) void w4a16_splitk_kernel(
         if (row >= m || col >= n) continue;
         const float vv[4] = {epilogue(v.x, bias, col, epi), epilogue(v.y, bias, col + 1, epi),
                              epilogue(v.z, bias, col + 2, epi), epilogue(v.w, bias, col + 3, epi)};
-        const size_t idx = out_index(row, col, col0, m, n, n_part);
+        const size_t idx = out_index(out.row_base + row, col, col0, out.m_out, out.n_out, n_part);
         if (out_type == QI_HIP_OUT_F16) {
             uint2 h;
             h.x = static_cast<uint32_t>(f2h(vv[0])) | (static_cast<uint32_t>(f2h(vv[1])) << 16);
@@ -553,13 +564,13 @@ __global__ __launch_bounds__(4 * WAVE) void w4a16_splitk_kernel(
 
 template <int TM, int TN>
 static int launch_splitk(const void *x, const void *codes, const void *scales, const float *bias, void *y,
-                         int out_type, int epi, int m, int n, int k, int n_part, hipStream_t stream) {
+                         int out_type, int epi, int m, int n, int k, int n_part, OutMap out, hipStream_t stream) {
     constexpr int BM = TM * 16, BN = TN * 16;
     const long long blocks = static_cast<long long>((m + BM - 1) / BM) * ((n + BN - 1) / BN);
     if (blocks > 0x7FFFFFFFLL) return kInvalid;
     w4a16_splitk_kernel<TM, TN><<<dim3(static_cast<unsigned>(blocks)), dim3(4 * WAVE), 0, stream>>>(
         static_cast<const uint16_t *>(x), static_cast<const uint8_t *>(codes), static_cast<const uint16_t *>(scales),
-        bias, y, out_type, epi, m, n, k, n_part);
+        bias, y, out_type, epi, m, n, k, n_part, out);
     return launch_status();
 }
 
@@ -602,9 +613,88 @@ QI_API int qi_w4a16_gemm(const void *x_half, const void *codes, const void *scal
                            nullptr);
 }
 
-QI_API int qi_hip_w4a16_gemm_tiled_parts(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
-                                         const float *bias, void *y, int out_type, int epilogue, int m, int n, int k,
-                                         int n_part, void *stream) {
+namespace qi {
+
+// Kernel shape for m rows and n_out outputs per stream (measured on
+// MI355X), and its launch.  m_split = 0: one stream (n = n_out).  m_split >
+// 0: the two streams' diagonal blocks over the stacked rows (n = 2 n_out
+// weight rows) in one launch when the chosen tiles fit both blocks, else
+// one launch per stream.  Arguments are checked by the callers; m > 16 per
+// stream.
+static int dispatch_w4a16(const void *x, const void *codes, const void *scales, const float *bias, void *y,
+                          int out_type, int epi, int m, int n, int k, int n_part, OutMap out, int m_split,
+                          hipStream_t s) {
+    const int n_out = out.n_out;
+    // QI_HIP_W4A16_TILES forces a shape, for tuning: 1 K-split 64 x 64, 2
+    // tiled 32 x 64, 3 tiled 64 x 64, 4 tiled 128 x 192.
+    static const int forced = [] {
+        const char *e = getenv("QI_HIP_W4A16_TILES");
+        return e ? atoi(e) : -1;
+    }();
+    int cfg;  // 1 K-split, 2..4 as above, 5 tiled 256 x 256, 6 tiled 128 x 128
+    if (forced >= 1 && forced <= 4 && (forced != 4 || n_out % 192 == 0))
+        cfg = forced;
+    // Short M with few column tiles (the text stream's 256 x 3072 outputs):
+    // the tiled grid is too small to fill the chip, so split K across the
+    // workgroup's waves instead (measured: 256 x 3072 x 3072 20.4 -> 17.5 us,
+    // 256 x 3072 x 12288 67.4 -> 49.3 us; wider N keeps the tiled kernel).
+    else if (m <= 256 && static_cast<long long>((m + 31) / 32) * ((n_out + 63) / 64) < 1024)
+        cfg = 1;
+    else if (m <= 256)
+        cfg = 2;  // short row tiles so the grid still covers the 256 CUs
+    else if (m <= 1024)
+        cfg = 3;
+    // 256 x 256 tiles (eight waves, one workgroup per CU: each weight is
+    // dequantised for twice the rows) when they still give three or more
+    // workgroups per CU; measured 11 % faster at 4096 x 12288 x 3072.
+    else if (n_out % 256 == 0 && static_cast<long long>((m + 255) / 256) * (n_out / 256) >= 768)
+        cfg = 5;
+    else if (n_out % 192 == 0)
+        cfg = 4;
+    else
+        cfg = 6;
+    const int bm[] = {0, 64, 32, 64, 128, 256, 128}, bn[] = {0, 64, 64, 64, 192, 256, 128};
+    // One launch over both streams only when its tiles fit both blocks and
+    // it takes no more rounds of workgroups than stream 0 alone (these
+    // kernels are not persistent: stream 1's tiles would otherwise run as an
+    // extra, mostly idle round).
+    bool one_launch = m_split > 0 && cfg != 1 && m_split % bm[cfg] == 0 && n_out % bn[cfg] == 0;
+    if (one_launch) {
+        const long long slots = static_cast<long long>(device_cus()) * (cfg == 5 ? 1 : 2);
+        const long long t0 = static_cast<long long>(m_split / bm[cfg]) * (n_out / bn[cfg]);
+        const long long t1 = static_cast<long long>((m - m_split + bm[cfg] - 1) / bm[cfg]) * (n_out / bn[cfg]);
+        one_launch = (t0 + t1 + slots - 1) / slots == (t0 + slots - 1) / slots;
+    }
+    if (m_split > 0 && !one_launch) {
+        // One launch per stream, each writing its rows of the stacked y.
+        const size_t g = static_cast<size_t>(k / 64);
+        int st = dispatch_w4a16(x, codes, scales, bias, y, out_type, epi, m_split, n_out, k, n_part,
+                                OutMap{out.row_base, out.m_out, n_out}, 0, s);
+        if (st) return st;
+        return dispatch_w4a16(static_cast<const uint16_t *>(x) + static_cast<size_t>(m_split) * k,
+                              static_cast<const uint8_t *>(codes) + static_cast<size_t>(n_out / 16) * g * 512,
+                              static_cast<const uint8_t *>(scales) + static_cast<size_t>(n_out / 16) * g * 64,
+                              bias ? bias + n_out : nullptr, y, out_type, epi, m - m_split, n_out, k, n_part,
+                              OutMap{out.row_base + m_split, out.m_out, n_out}, 0, s);
+    }
+    switch (cfg) {
+    case 1:
+        return launch_splitk<4, 4>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, s);
+    case 2:
+        return launch_tiled<2, 1, 4>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, m_split, s);
+    case 3:
+        return launch_tiled<4, 1, 4>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, m_split, s);
+    case 4:
+        return launch_tiled<8, 3, 4>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, m_split, s);
+    case 5:
+        return launch_tiled<16, 2, 8>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, m_split, s);
+    default:
+        return launch_tiled<8, 2, 4>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, m_split, s);
+    }
+}
+
+static int check_w4a16_args(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales, const void *y,
+                            int out_type, int epilogue, int m, int n, int k, int n_part) {
     if (m <= 0 || n <= 0 || k <= 0 || n % 16 || k % 64) return kInvalid;
     if (n_part <= 0 || n_part % 16 || n % n_part) return kInvalid;
     if (!x_half || !w_tiled_codes || !w_tiled_scales || !y) return kInvalid;
@@ -613,6 +703,16 @@ QI_API int qi_hip_w4a16_gemm_tiled_parts(const void *x_half, const void *w_tiled
     if (reinterpret_cast<uintptr_t>(x_half) % 16 || reinterpret_cast<uintptr_t>(w_tiled_codes) % 8 ||
         reinterpret_cast<uintptr_t>(w_tiled_scales) % 4 || k % 8)
         return kInvalid;
+    return 0;
+}
+
+}  // namespace qi
+
+QI_API int qi_hip_w4a16_gemm_tiled_parts(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
+                                         const float *bias, void *y, int out_type, int epilogue, int m, int n, int k,
+                                         int n_part, void *stream) {
+    if (const int st = check_w4a16_args(x_half, w_tiled_codes, w_tiled_scales, y, out_type, epilogue, m, n, k, n_part))
+        return st;
     if (m <= 16) {
         // One GEMV per part: a part is n_part / 16 whole weight tiles.
         const size_t tile_codes = static_cast<size_t>(k / 64) * 64 * 8, tile_scales = static_cast<size_t>(k / 64) * 64;
@@ -629,50 +729,20 @@ QI_API int qi_hip_w4a16_gemm_tiled_parts(const void *x_half, const void *w_tiled
     }
     if (static_cast<long long>(m) * k * 2 >= (1LL << 32) || static_cast<long long>(n) * (k / 2) >= (1LL << 32))
         return kInvalid;
-    // Small m: short row tiles so the grid still covers the 256 CUs.
-    // Short M with few column tiles (the text stream's 256 x 3072 outputs):
-    // the tiled grid is too small to fill the chip, so split K across the
-    // workgroup's waves instead (measured on MI355X: 256 x 3072 x 3072 20.4
-    // -> 17.5 us, 256 x 3072 x 12288 67.4 -> 49.3 us; wider N keeps the tiled
-    // kernel).
-    // QI_HIP_W4A16_TILES forces a shape, for tuning: 1 K-split 64 x 64, 2
-    // tiled 32 x 64, 3 tiled 64 x 64, 4 tiled 128 x 192.
-    static const int forced = [] {
-        const char *e = getenv("QI_HIP_W4A16_TILES");
-        return e ? atoi(e) : -1;
-    }();
-    if (forced == 1)
-        return launch_splitk<4, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k, n_part,
-                                   stream_of(stream));
-    if (forced == 2)
-        return launch_tiled<2, 1, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
-                                     n_part, stream_of(stream));
-    if (forced == 3)
-        return launch_tiled<4, 1, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
-                                     n_part, stream_of(stream));
-    if (forced == 4 && n % 192 == 0)
-        return launch_tiled<8, 3, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
-                                     n_part, stream_of(stream));
-    if (m <= 256 && static_cast<long long>((m + 31) / 32) * ((n + 63) / 64) < 1024)
-        return launch_splitk<4, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k, n_part,
-                                   stream_of(stream));
-    if (m <= 256)
-        return launch_tiled<2, 1, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k, n_part,
-                                     stream_of(stream));
-    if (m <= 1024)
-        return launch_tiled<4, 1, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k, n_part,
-                                     stream_of(stream));
-    // 256 x 256 tiles (eight waves, one workgroup per CU: each weight is
-    // dequantised for twice the rows) when they still give three or more
-    // workgroups per CU; measured 11 % faster at 4096 x 12288 x 3072.
-    if (n % 256 == 0 && static_cast<long long>((m + 255) / 256) * (n / 256) >= 768)
-        return launch_tiled<16, 2, 8>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k, n_part,
-                                      stream_of(stream));
-    if (n % 192 == 0)
-        return launch_tiled<8, 3, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k, n_part,
-                                     stream_of(stream));
-    return launch_tiled<8, 2, 4>(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k, n_part,
-                                 stream_of(stream));
+    return dispatch_w4a16(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k, n_part,
+                          OutMap{0, m, n}, 0, stream_of(stream));
+}
+
+QI_API int qi_hip_w4a16_gemm_tiled_dual(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
+                                        const float *bias, void *y, int out_type, int epilogue, int m, int m_split,
+                                        int n, int k, int n_part, void *stream) {
+    if (const int st = check_w4a16_args(x_half, w_tiled_codes, w_tiled_scales, y, out_type, epilogue, m, n, k, n_part))
+        return st;
+    if (m_split <= 16 || m - m_split <= 16) return kInvalid;
+    if (static_cast<long long>(m) * k * 2 >= (1LL << 32) || static_cast<long long>(2 * n) * (k / 2) >= (1LL << 32))
+        return kInvalid;
+    return dispatch_w4a16(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, 2 * n, k, n_part,
+                          OutMap{0, m, n}, m_split, stream_of(stream));
 }
 
 QI_API int qi_hip_w4a16_gemm_tiled(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,

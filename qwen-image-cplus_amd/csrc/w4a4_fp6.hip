@@ -63,14 +63,8 @@ __device__ __forceinline__ v8i fp6_operand(v4i lo, v4i hi) {
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 4, 5, 6, -1, -1);
 }
 
-// Where outputs go.  Output (row, col) of the GEMM is element
-// (row_base + row, col - fold) of a y made of n_out / n_part parts of
-// [m_out, n_part] (out_index), where fold = n_out for the second stream's
-// columns (col >= n_out) of a dual-stream call and 0 otherwise.  A plain call
-// has row_base 0, m_out = m, n_out = n.
-struct Fp6Out {
-    int row_base, m_out, n_out;
-};
+using Fp6Out = OutMap;
+using Fp6Grid = TileGrid2;
 
 template <int TM, int TN, int WM, int WN, int NSTAGE>
 struct Fp6Shape {
@@ -438,25 +432,6 @@ __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2)
 // is computed once into LDS, outside the pipelined loop.
 constexpr int FP6_MAX_TILES = 128;
 
-// The 128 x 128 tile grid of a persistent call: t0 = tm0 * tn0 tiles of
-// stream 0 (tile rows from 0, tile columns from 0), then tm1 * tn1 tiles of
-// stream 1 (tile rows from tm0, columns from tn0) -- the two diagonal blocks
-// of a dual-stream call.  A plain call has tm1 = tn1 = 0.
-struct Fp6Grid {
-    int t0, tm0, tn0, tm1, tn1;
-};
-
-// 128 x 128 tile t of the grid, in XCD-aware order within each stream.
-__device__ __forceinline__ void grid_tile(const Fp6Grid &gd, int t, int &tm, int &tn) {
-    if (t < gd.t0) {
-        tile_of_block(t, gd.tm0, gd.tn0, 8, tm, tn);
-    } else {
-        tile_of_block(t - gd.t0, gd.tm1, gd.tn1, 8, tm, tn);
-        tm += gd.tm0;
-        tn += gd.tn0;
-    }
-}
-
 template <int TN, int WM, int WN, int NSTAGE>
 __global__ __launch_bounds__(WM *WN *WAVE) __attribute__((amdgpu_waves_per_eu(2))) void w4a4_fp6_persistent_kernel(
     const uint8_t *__restrict__ a6, const uint8_t *__restrict__ w6, const float *__restrict__ bias,
@@ -515,19 +490,6 @@ static int launch_fp6(const void *a6, const void *w6, const float *bias, void *y
         static_cast<const uint8_t *>(a6), static_cast<const uint8_t *>(w6), bias, y, out_type, epi, m, n, k, n_part,
         out);
     return launch_status();
-}
-
-// Compute units of the current device, read once per device.
-static int device_cus() {
-    static int cus[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cus[dev] == 0) {
-        int c = 0;
-        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
-        cus[dev] = c;
-    }
-    return cus[dev];
 }
 
 // 128 x 128 tiles, two workgroups per CU, persistent (see the kernel); m,

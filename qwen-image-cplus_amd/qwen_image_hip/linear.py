@@ -58,19 +58,20 @@ class PackedLinear:
     def dual(cls, records: "list[PackedLinear]") -> "PackedLinear":
         """The image and text streams' records of one MMDiT block linear
         (same shape), run by one call over the stacked rows of both streams
-        (``linear(..., split_rows=image_rows)``); fp6 W4A4 records only."""
+        (``linear(..., split_rows=image_rows)``); fp6 W4A4 or W4A16 records."""
         if len(records) != 2:
             raise ValueError("a dual-stream record pairs exactly two records")
         a, b = records
         if (a.scheme, a.n, a.k, a.operand, a.parts, a.streams) != (b.scheme, b.n, b.k, b.operand, b.parts, 1) \
                 or a.streams != 1:
             raise ValueError("dual-stream records need one scheme, shape and operand format")
-        if a.scheme != SCHEME_W4A4_H256 or a.operand != W4A4_FP6:
-            raise ValueError("dual-stream records run on the fp6 W4A4 path")
+        if a.scheme == SCHEME_W4A4_H256 and a.operand != W4A4_FP6:
+            raise ValueError("dual-stream W4A4 records run on the fp6 operand format")
         if (a.bias is None) != (b.bias is None):
             raise ValueError("either both records have a bias or neither has")
         bias = None if a.bias is None else torch.cat([a.bias, b.bias], 0)
-        return cls(a.scheme, a.n, a.k, torch.cat([a.tiled_codes, b.tiled_codes], 0), None, bias, a.operand,
+        ts = None if a.tiled_scales is None else torch.cat([a.tiled_scales, b.tiled_scales], 0)
+        return cls(a.scheme, a.n, a.k, torch.cat([a.tiled_codes, b.tiled_codes], 0), ts, bias, a.operand,
                    a.parts, 2)
 
     @classmethod
@@ -205,6 +206,11 @@ def linear(record: PackedLinear, work: Work, input: torch.Tensor, output: torch.
             if not reuse_input:
                 ops.f32_to_f16(input[:rows], halves)
             x_half = halves
+        if record.streams == 2:
+            if split_rows is None:
+                raise ValueError("a dual-stream record needs split_rows")
+            return ops.w4a16_gemm_dual(x_half, record.tiled_codes, record.tiled_scales, split_rows, record.bias,
+                                       out_dtype, gelu, output, n_part)
         return ops.w4a16_gemm(x_half, record.tiled_codes, record.tiled_scales, record.bias, out_dtype, gelu,
                               output, n_part)
     raise ValueError(f"unsupported scheme {record.scheme}")

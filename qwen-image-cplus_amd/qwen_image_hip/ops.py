@@ -189,6 +189,22 @@ def w4a16_gemm(x_half, w_tiled_codes, w_tiled_scales, bias=None, out_dtype=torch
     return y
 
 
+def w4a16_gemm_dual(x_half, w_tiled_codes, w_tiled_scales, m_split: int, bias=None, out_dtype=torch.float32,
+                    gelu=False, y=None, n_part=None):
+    """Both streams of a dual-stream block (qi_hip_w4a16_gemm_tiled_dual):
+    rows < m_split use the first half of the weight rows, the others the
+    second; y is [m, n] (or [n / n_part, m, n_part]), n = weight rows / 2."""
+    m, k = x_half.shape
+    n = w_tiled_codes.shape[0] // 2
+    out_type = OUT_F16 if out_dtype == torch.float16 else OUT_F32
+    y = y if y is not None else _empty(_out_shape(m, n, n_part), out_dtype, x_half)
+    st = load().qi_hip_w4a16_gemm_tiled_dual(_ptr(x_half), _ptr(w_tiled_codes), _ptr(w_tiled_scales), _ptr(bias),
+                                             _ptr(y), out_type, EPILOGUE_GELU_TANH if gelu else EPILOGUE_NONE, m,
+                                             m_split, n, k, n if n_part is None else n_part, _stream())
+    check(st, "w4a16 gemm")
+    return y
+
+
 def w4a16_gemv(x_half, w_tiled_codes, w_tiled_scales, bias=None, out_dtype=torch.float32, gelu=False, y=None):
     m, k = x_half.shape
     n = w_tiled_codes.shape[0]

@@ -77,6 +77,9 @@ def test_extension_argument_checks():
     assert L.qi_hip_w4a4_gemm_fp6_dual(16, 16, None, 16, 0, 0, 256, 0, 64, 256, 64, None) == INVALID
     assert L.qi_hip_w4a4_gemm_fp6_dual(16, 16, None, 16, 0, 0, 256, 256, 64, 256, 64, None) == INVALID
     assert L.qi_hip_w4a4_gemm_fp6_dual(16, 16, None, 16, 0, 0, 256, 40, 64, 256, 64, None) == INVALID
+    # W4A16 dual-stream: each stream needs more than 16 rows
+    assert L.qi_hip_w4a16_gemm_tiled_dual(16, 8, 8, None, 16, 0, 0, 100, 16, 64, 64, 64, None) == INVALID
+    assert L.qi_hip_w4a16_gemm_tiled_dual(16, 8, 8, None, 16, 0, 0, 100, 90, 64, 64, 64, None) == INVALID
     # producers: widths, alignment, output types, scratch
     assert L.qi_hip_layer_norm_scale(16, 16, 16, 16, 0, 4, 30, 0, None) == INVALID          # width % 4
     assert L.qi_hip_layer_norm_scale(16, 16, 16, 16, 2, 4, 32, 0, None) == INVALID          # out type

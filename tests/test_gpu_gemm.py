@@ -357,3 +357,31 @@ def test_w4a16_fused_record_matches_separate_records(dev, m):
             torch.testing.assert_close(got[i], want, rtol=0, atol=0)
         else:
             _close(got[i].cpu().numpy(), want.cpu().numpy())
+
+
+@pytest.mark.parametrize("m_img,m_txt", [(4096, 256), (320, 40)])
+def test_w4a16_dual_stream_record_matches_per_stream_calls(dev, m_img, m_txt):
+    """The image and text streams' fused W4A16 records as one dual-stream
+    call on the stacked rows, against each stream's own call: within the
+    W4A16 tolerance (the kernel shape is chosen for the stacked rows; 320 +
+    40 runs one launch over both streams), and bit-identical for the image
+    rows at 4096 + 256, which runs one launch per stream."""
+    import qwen_image_hip as q
+    n, k = 1536, 1024
+    m = m_img + m_txt
+    print(f"w4a16 dual stream m={m_img}+{m_txt}", flush=True)
+    x = _h(f16_bits(normal_f32(m, k, 760 + m)), dev)
+    recs = []
+    for s in range(2):
+        parts = [q.PackedLinear.from_fp16(q.SCHEME_W4A16, _h(weights_f16(n, k, 761 + 10 * s + i), dev))
+                 for i in range(3)]
+        recs.append(q.PackedLinear.fuse(parts))
+    pair = q.PackedLinear.dual(recs)
+    work = q.Work(m, k, dev)
+    got = q.linear(pair, work, x, out_dtype=torch.float32, split_rows=m_img)
+    want0 = q.linear(recs[0], work, x[:m_img], out_dtype=torch.float32)
+    want1 = q.linear(recs[1], work, x[m_img:].contiguous(), out_dtype=torch.float32)
+    _close(got[:, :m_img].cpu().numpy(), want0.cpu().numpy())
+    _close(got[:, m_img:].cpu().numpy(), want1.cpu().numpy())
+    if m_img == 4096:
+        torch.testing.assert_close(got[:, :m_img], want0, rtol=0, atol=0)
