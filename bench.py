@@ -393,6 +393,26 @@ def bench_producers(iters=50):
     return out
 
 
+def bench_attention(iters=20):
+    """The block's joint attention at 1024x1024: 4096 image + 256 text tokens,
+    24 heads of 128, no mask (qi_flash_attention's work in the reference,
+    transformer.cplus:802-803); FLOPs = 4 * tokens^2 * 128 * heads."""
+    import torch
+    from qwen_image_hip import ops
+
+    n, heads = sum(STREAMS.values()), HIDDEN // 128
+    g = torch.Generator(device="cuda")
+    g.manual_seed(77)
+    q = torch.randn((n, HIDDEN), generator=g, device="cuda")
+    k = torch.randn((n, HIDDEN), generator=g, device="cuda").half()
+    v = torch.randn((n, HIDDEN), generator=g, device="cuda").half()
+    out = torch.empty_like(q)
+    ms = time_fn(lambda: ops.flash_attention(q, k, v, heads, out=out), iters, 3)
+    flops = 4.0 * n * n * 128 * heads
+    return {"tokens": n, "heads": heads, "us": round(ms * 1e3, 1), "TFLOP_s": round(flops / (ms * 1e-3) / 1e12, 1),
+            "frac_fp16_peak": round(flops / (ms * 1e-3) / PEAK_FP16_FLOPS, 4)}
+
+
 ENCODER_ROWS = 300  # config 4: prompt tokens through the Qwen2.5-VL-7B-shaped text encoder
 ENCODER_SHAPES = [("q", 3584, 3584), ("k+v fused", 2 * 512, 3584), ("gate+up fused", 2 * 18944, 3584),
                   ("down", 3584, 18944)]
@@ -655,6 +675,8 @@ def main(argv=None) -> int:
         log(f"gemv: {extra['modulation_gemv']}")
         extra["producers"] = bench_producers()
         log(f"producers: {extra['producers']}")
+        extra["attention"] = bench_attention()
+        log(f"attention: {extra['attention']}")
         extra["encoder_w4a16_m300"] = bench_encoder()
         log(f"encoder: {extra['encoder_w4a16_m300']}")
         if not args.no_stack:

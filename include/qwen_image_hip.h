@@ -235,6 +235,21 @@ int qi_hip_swiglu(const float *gate, const float *up, void *out, int out_type, u
                   void *stream);
 int qi_hip_swiglu_quantize_fp6(const float *gate, const float *up, void *codes6, int m, int k, void *stream);
 
+/* Fused attention (the reference's qi_flash_attention, qwen_image_cuda/
+ * cuda/flash.cu:237-244, same arguments and layouts): head dim 128; q and
+ * out fp32 [queries, heads * 128], k_half and v_half fp16 [keys, heads *
+ * 128]; row r (global r + query_offset) sees keys [0, visible_keys[r]) when
+ * visible_keys (device int array indexed by global row) is given, else
+ * [0, r + 1) when r < causal_rows, else every key; rows with nothing visible
+ * get 0.  Q is scaled by log2(e) / sqrt(128) and rounded to fp16, the
+ * softmax runs online in the log2 domain with fp16 probabilities in the
+ * P V product.  Pointers 16-byte aligned.  qi_flash_attention runs on the
+ * null stream, as the reference does. */
+int qi_flash_attention(const float *q, const void *k_half, const void *v_half, float *out, int queries, int keys,
+                       int heads, int query_offset, int causal_rows, const int *visible_keys);
+int qi_hip_flash_attention(const float *q, const void *k_half, const void *v_half, float *out, int queries, int keys,
+                           int heads, int query_offset, int causal_rows, const int *visible_keys, void *stream);
+
 /* Device-side QIPACK quantiser (int4_pack.cplus:237-468 arithmetic, bit-exact):
  * w_half fp16 [n, k] -> QIPACK arrays.  scheme 5 = W4A16 affine (minimums
  * required), scheme 6 = W4A4 H256 symmetric (minimums ignored).  group must

@@ -217,3 +217,40 @@ def swiglu(gate, up) -> np.ndarray:
     """silu(gate) * up in float64 (qwen_image_cuda/cuda/ops.cu:134-139)."""
     g = np.asarray(gate, np.float64)
     return g / (1.0 + np.exp(-g)) * np.asarray(up, np.float64)
+
+
+def flash_attention(q, k_bits, v_bits, heads: int, query_offset: int = 0, causal_rows: int = 0,
+                    visible_keys=None, round_p: bool = True) -> np.ndarray:
+    """The reference's fused attention in float64 (qwen_image_cuda/cuda/flash.cu:
+    1-244): head dim 128; q fp32 [Q, heads*128] is scaled by log2(e)/sqrt(128) in
+    fp32 and rounded to fp16 (:86-97); k, v are fp16 bits [K, heads*128]; row r
+    (global r + query_offset) sees keys [0, visible_keys[r]) or, without that
+    array, [0, r + 1) when r < causal_rows, else all (:46-49); softmax in the
+    log2 domain; the P V product uses fp16 probabilities (round_p) while the
+    sum adds the unrounded ones (:178-186); rows with nothing visible give 0."""
+    d = 128
+    q = np.asarray(q, np.float32)
+    nq, nk = q.shape[0], np.asarray(k_bits).shape[0]
+    scale = np.float32(1.4426950408889634) / np.sqrt(np.float32(d))
+    qs = half_to_f32(half_from_f32(q * scale)).astype(np.float64)
+    k = half_to_f32(k_bits).astype(np.float64)
+    v = half_to_f32(v_bits).astype(np.float64)
+    rows = np.arange(nq) + query_offset
+    if visible_keys is not None:
+        vis = np.minimum(np.asarray(visible_keys)[rows], nk)
+    else:
+        vis = np.where(rows < causal_rows, rows + 1, nk)
+    mask = np.arange(nk)[None, :] < vis[:, None]
+    out = np.zeros((nq, heads * d))
+    for h in range(heads):
+        sl = slice(h * d, (h + 1) * d)
+        s = qs[:, sl] @ k[:, sl].T
+        s = np.where(mask, s, -np.inf)
+        m = s.max(axis=1, keepdims=True)
+        m = np.where(np.isfinite(m), m, 0.0)
+        p = np.exp2(s - m)
+        tot = p.sum(axis=1, keepdims=True)
+        pv = half_to_f32(half_from_f32(p.astype(np.float32))).astype(np.float64) if round_p else p
+        o = pv @ v[:, sl]
+        out[:, sl] = np.where(tot > 0, o / np.where(tot > 0, tot, 1.0), 0.0)
+    return out

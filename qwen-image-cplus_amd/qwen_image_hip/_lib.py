@@ -40,6 +40,8 @@ SIGNATURES: dict[str, list] = {
     "qi_hip_w4a4_gemm_fp6_dual": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p],
     "qi_hip_w4a16_gemm_tiled_parts": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p],
     "qi_hip_w4a16_gemm_tiled_dual": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p],
+    "qi_flash_attention": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
+    "qi_hip_flash_attention": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p],
     "qi_hip_layer_norm_scale": [_p, _p, _i, _p, _i, _i, _i, _i, _p],
     "qi_hip_layer_norm_scale_quantize_fp6": [_p, _p, _i, _i, _p, _p, _i, _i, _p],
     "qi_hip_swiglu": [_p, _p, _p, _i, _u64, _p],

@@ -341,3 +341,25 @@ def swiglu_quantize_fp6(gate: torch.Tensor, up: torch.Tensor, codes6: torch.Tens
     check(load().qi_hip_swiglu_quantize_fp6(_ptr(gate), _ptr(up), _ptr(codes6), m, k, _stream()),
           "swiglu quantization")
     return codes6
+
+
+# --------------------------------------------------------------- attention --
+
+
+def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, heads: int, query_offset: int = 0,
+                    causal_rows: int = 0, visible_keys: torch.Tensor | None = None,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused attention, head dim 128 (reference qi_flash_attention,
+    qwen_image_cuda/cuda/flash.cu): q fp32 [queries, heads*128], k and v fp16
+    [keys, heads*128]; visible_keys an int32 device tensor indexed by global row."""
+    nq, width = q.shape
+    if q.dtype != torch.float32 or k.dtype != torch.float16 or v.dtype != torch.float16:
+        raise TypeError("q fp32, k and v fp16")
+    if width != heads * 128 or k.shape[1] != width or v.shape != k.shape:
+        raise ValueError("q, k, v must be [rows, heads * 128]")
+    if visible_keys is not None and visible_keys.dtype != torch.int32:
+        raise TypeError("visible_keys must be int32")
+    out = out if out is not None else _empty((nq, width), torch.float32, q)
+    check(load().qi_hip_flash_attention(_ptr(q), _ptr(k), _ptr(v), _ptr(out), nq, k.shape[0], heads, query_offset,
+                                        causal_rows, _ptr(visible_keys), _stream()), "attention")
+    return out

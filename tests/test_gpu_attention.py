@@ -1,0 +1,81 @@
+"""GPU parity of the fused attention (reference qi_flash_attention,
+qwen_image_cuda/cuda/flash.cu) against the float64 oracle on small shapes
+(every mask form, ragged tiles, rows with nothing visible) and against a
+torch fp32 restatement at the 1024x1024 block's full size."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _data import MAX_ABS_RMS_TOL, REL_L2_TOL, max_abs_over_rms, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(nq, nk, heads, seed):
+    rng = np.random.default_rng(seed)
+    q = rng.normal(0, 1.5, size=(nq, heads * 128)).astype(np.float32)
+    k = oracle.half_from_f32(rng.normal(0, 1, size=(nk, heads * 128)).astype(np.float32))
+    v = oracle.half_from_f32(rng.normal(0, 1, size=(nk, heads * 128)).astype(np.float32))
+    return q, k, v
+
+
+def _run(dev, q, k, v, heads, **kw):
+    import qwen_image_hip.ops as ops
+    vis = kw.pop("visible_keys", None)
+    vd = None if vis is None else torch.from_numpy(np.asarray(vis, np.int32)).to(dev)
+    return ops.flash_attention(torch.from_numpy(q).to(dev), torch.from_numpy(k).to(dev).view(torch.float16),
+                               torch.from_numpy(v).to(dev).view(torch.float16), heads, visible_keys=vd,
+                               **kw).cpu().numpy()
+
+
+def _close(got, want):
+    assert rel_l2(got, want) <= REL_L2_TOL, rel_l2(got, want)
+    assert max_abs_over_rms(got, want) <= MAX_ABS_RMS_TOL, max_abs_over_rms(got, want)
+
+
+@pytest.mark.parametrize("nq,nk,heads", [(1, 64, 1), (200, 300, 3), (129, 1000, 2)])
+def test_attention_unmasked(dev, nq, nk, heads):
+    print(f"attention nq={nq} nk={nk} heads={heads}", flush=True)
+    q, k, v = _case(nq, nk, heads, 1000 + nq)
+    _close(_run(dev, q, k, v, heads), oracle.flash_attention(q, k, v, heads))
+
+
+def test_attention_causal_and_offset(dev):
+    q, k, v = _case(257, 400, 2, 1100)
+    got = _run(dev, q, k, v, 2, query_offset=50, causal_rows=200)
+    want = oracle.flash_attention(q, k, v, 2, query_offset=50, causal_rows=200)
+    _close(got, want)
+    # global row 50 + 0 < 200 sees 51 keys; rows from 150 on see all 400
+    np.testing.assert_allclose(got[0], want[0], rtol=5e-3, atol=5e-3)
+
+
+def test_attention_visible_keys_and_empty_rows(dev):
+    q, k, v = _case(96, 130, 2, 1200)
+    vis = np.random.default_rng(1201).integers(0, 131, size=96)
+    vis[[0, 7, 40]] = 0                       # nothing visible: output 0
+    vis[[1, 2]] = 1                           # one key: its value row
+    got = _run(dev, q, k, v, 2, visible_keys=vis)
+    want = oracle.flash_attention(q, k, v, 2, visible_keys=vis)
+    assert (got[[0, 7, 40]] == 0).all()
+    np.testing.assert_array_equal(got[1], oracle.half_to_f32(v[0]))
+    _close(got, want)
+
+
+def test_attention_full_block_size_vs_torch_fp32(dev):
+    """4352 tokens (4096 image + 256 text), 24 heads: against torch fp32 on
+    the same fp16-rounded scaled q and fp16 k, v (softmax in fp32)."""
+    import qwen_image_hip.ops as ops
+    n, heads = 4352, 24
+    g = torch.Generator(device=dev)
+    g.manual_seed(1300)
+    q = torch.randn((n, heads * 128), generator=g, device=dev) * 1.5
+    k = torch.randn((n, heads * 128), generator=g, device=dev).half()
+    v = torch.randn((n, heads * 128), generator=g, device=dev).half()
+    got = ops.flash_attention(q, k, v, heads)
+    scale = np.float32(1.4426950408889634) / np.sqrt(np.float32(128))
+    qs = (q * float(scale)).half().float().view(n, heads, 128).transpose(0, 1)
+    s = torch.bmm(qs, k.float().view(n, heads, 128).permute(1, 2, 0))          # log2-domain scores
+    p = torch.softmax(s * float(np.log(2.0)), dim=-1)
+    want = torch.bmm(p, v.float().view(n, heads, 128).transpose(0, 1)).transpose(0, 1).reshape(n, heads * 128)
+    _close(got.cpu().numpy(), want.cpu().numpy())

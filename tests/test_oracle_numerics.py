@@ -373,3 +373,43 @@ def test_swiglu_oracle_known_values():
     np.testing.assert_allclose(oracle.swiglu(g, u), g * expit(g) * u, rtol=1e-14)
     assert oracle.swiglu(np.array([0.0]), np.array([5.0]))[0] == 0.0
     np.testing.assert_allclose(oracle.swiglu(np.array([40.0]), np.array([1.0])), [40.0], rtol=1e-15)
+
+
+# ------------------------------------------------------------- attention --
+
+def _att_inputs(nq, nk, heads, seed):
+    rng = np.random.default_rng(seed)
+    q = rng.normal(0, 1, size=(nq, heads * 128)).astype(np.float32)
+    k = oracle.half_from_f32(rng.normal(0, 1, size=(nk, heads * 128)).astype(np.float32))
+    v = oracle.half_from_f32(rng.normal(0, 1, size=(nk, heads * 128)).astype(np.float32))
+    return q, k, v
+
+
+def test_attention_oracle_closed_forms():
+    from scipy.special import softmax
+    q, k, v = _att_inputs(5, 7, 2, 21)
+    vf = oracle.half_to_f32(v).astype(np.float64)
+    # identical keys: uniform weights, out = mean of the visible values
+    k_same = np.tile(k[:1], (7, 1))
+    out = oracle.flash_attention(q, k_same, v, 2, round_p=False)
+    np.testing.assert_allclose(out, np.tile(vf.mean(axis=0), (5, 1)), rtol=1e-12, atol=1e-12)
+    # one visible key: out = that key's value row (p = 1 exactly)
+    out = oracle.flash_attention(q, k, v, 2, visible_keys=np.ones(5, np.int64))
+    np.testing.assert_allclose(out, np.tile(vf[0], (5, 1)), rtol=0, atol=0)
+    # causal rows: row r sees r + 1 keys; nothing visible gives 0
+    out = oracle.flash_attention(q, k, v, 2, causal_rows=5)
+    np.testing.assert_allclose(out[0], vf[0], rtol=0, atol=0)
+    vis = np.array([0, 3, 7, 2, 0])
+    out = oracle.flash_attention(q, k, v, 2, visible_keys=vis)
+    assert (out[0] == 0).all() and (out[4] == 0).all()
+    # against scipy's softmax over the natural-log scores of the fp16 inputs
+    qs = oracle.half_to_f32(oracle.half_from_f32(q * (np.float32(1.4426950408889634) / np.sqrt(np.float32(128)))))
+    kf = oracle.half_to_f32(k).astype(np.float64)
+    want = np.zeros((5, 256))
+    for h in range(2):
+        sl = slice(128 * h, 128 * h + 128)
+        w = softmax((qs[:, sl].astype(np.float64) @ kf[:, sl].T) * np.log(2.0), axis=1)
+        want[:, sl] = w @ vf[:, sl]
+    np.testing.assert_allclose(oracle.flash_attention(q, k, v, 2, round_p=False), want, rtol=1e-10, atol=1e-12)
+    # fp16 probabilities move the result by ~2^-11 relative at most
+    np.testing.assert_allclose(oracle.flash_attention(q, k, v, 2), want, rtol=0, atol=2e-3)
