@@ -348,7 +348,6 @@ __device__ __forceinline__ void fp6_tiles(uint8_t *lds, const uint8_t *__restric
         }
     };
     using Mid = std::false_type;
-    using Last = std::true_type;
 
     zero_acc();
     set_tile_loads(0);
