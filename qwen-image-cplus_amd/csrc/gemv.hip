@@ -5,14 +5,16 @@
 // to follow, so the arithmetic is the W4A16 GEMM's weights
 // (qwen_image_cuda/cuda/gemm.cu:222-230) within the W4A16 tolerance.
 //
-// Layout: one workgroup owns one 16-row weight tile; in the tiled layout the
+// Layout (matrix-core forms): one workgroup owns one 16-row weight tile; in the tiled layout the
 // tile's groups are consecutive 512-byte blocks, and each of the four
 // wavefronts streams a contiguous quarter of them, with batches of groups of
 // loads (one 8-byte code load and one scale pair per lane each) in flight.
 // The activations are staged in LDS, and the wavefronts' partial sums are
 // added through LDS.  Three kernels:
 //   * w4a16_gemv_dot2_kernel (m = 1, 2): vector unit, dot2 on the fp16
-//     integers 1024 + c with the factored per-group scale step;
+//     integers 1024 + c with the factored per-group scale step, two weight
+//     rows per lane and a wave-local x slice (its own layout, described at
+//     the kernel);
 //   * w4a16_gemv_factored_kernel (m <= 16, x fits in LDS): the same
 //     factored form on the matrix core (16 rows per MFMA);
 //   * w4a16_gemv_kernel: dequantised fp16 weights (the GEMM's exact weights)
@@ -258,124 +260,140 @@ __global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_factored_kernel(
 }
 
 // Vector-unit form for m <= 2 (the modulation linears' one or two rows),
-// where a 16-row MFMA would waste most of its work.  The factored arithmetic
-// of the kernel above, per lane: lane l of a 16-row tile holds 16 codes of
-// row l % 16 per group (elements 8q .. 8q+7 and 32+8q .. 32+8q+7, q = l / 16,
-// each pair (2i, 2i+1) one nibble-pair slot), inserts them into 0x6400 as the
-// fp16 integers 1024 + c, and forms P_l = sum x (1024 + c) over its 16
-// inputs with v_dot2_f32_f16 (fp16 products exact in fp32).  With X_l the sum
-// of the same 16 inputs (precomputed once per workgroup in LDS), the lane's
-// share of the group is s (P_l - 1024 X_l) + min X_l; the shares are summed
-// per lane over its groups, then over the four lanes of a row and the
-// workgroup's waves.  This is the group's dot product with the weights
-// c s + min in fp32, like the MFMA form: inside the W4A16 tolerance, and
-// bit-exact fp32(c s + min) on one-hot rows.
+// where a 16-row MFMA would waste most of its work.  The kernel is bound by
+// the weight stream at first and then by what follows the last arrival, so it
+// keeps every latency chain off that path:
+//   * lane l loads 16 bytes of a 1 KB pair of group blocks: slots 2j and
+//     2j + 1 (j = l % 32) of group gc + 2u + l / 32, i.e. rows 2j % 16 and
+//     2j % 16 + 1 with the same input chunk q = j / 8, so one read of x from
+//     LDS serves two weight rows;
+//   * each wave stages only its own slice of x (its groups, requested before
+//     the weights, stored once it lands), so no workgroup barrier precedes
+//     the arithmetic;
+//   * the codes enter v_dot2_f32_f16 as the fp16 integers 1024 + c (a
+//     bit-field insert into 0x6400), and the lane's share of a group is
+//     s (P - 1024 X) + min X with P = sum x (1024 + c) and X = sum x over
+//     the lane's 16 inputs (the same dot2 against ones);
+//   * the lanes of a row differ in lane bits 3..5: bit 3 is folded by a DPP
+//     row rotate, bits 4..5 and the waves through one LDS pass.
+// This is the group's dot product with the weights c s + min in fp32, like
+// the MFMA forms: inside the W4A16 tolerance, and bit-exact fp32(c s + min) on
+// one-hot rows.
+constexpr int DOT2_WAVES = 8;
+constexpr int DOT2_FB = 6;  // groups per wave and chunk: three 16-byte loads per lane
+
 template <int M>
-__global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_dot2_kernel(
+__global__ __launch_bounds__(DOT2_WAVES *WAVE) void w4a16_gemv_dot2_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
     const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int n, int k) {
-    __shared__ float partial[GEMV_WAVES][M][16];
-    extern __shared__ __attribute__((aligned(16))) uint16_t xs_lds[];  // M * k fp16, then M * k / 16 fp32 sums
-    float *xsum = reinterpret_cast<float *>(xs_lds + M * k);
+    constexpr int W = DOT2_WAVES, FB = DOT2_FB, NI = FB / 2;
+    constexpr int XC = M * FB * 8;  // 16-byte chunks of a wave's x slice
+    constexpr int XR = (XC + WAVE - 1) / WAVE;
+    __shared__ float partial[W][4][M][16];
+    __shared__ __attribute__((aligned(16))) uint16_t xs[W][M * FB * 64];
     const int groups = k >> 6;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
-    const int q = lane >> 4, r16 = lane & 15;
+    const int h = lane >> 5, j = lane & 31, q = j >> 3, r0 = (2 * j) & 15;
     const int tile = blockIdx.x;
-
-    const int per_wave = (groups + GEMV_WAVES - 1) / GEMV_WAVES;
-    const int g_begin = wave * per_wave;
-    const int g_end = min(groups, g_begin + per_wave);
-    const uint8_t *cp = codes + static_cast<size_t>(tile) * groups * 512 + lane * 8;
-    // The (scale, minimum) pair of the lane's own row.
-    const uint32_t *sp = reinterpret_cast<const uint32_t *>(scales) + static_cast<size_t>(tile) * groups * 16 + r16;
-
-    // Batches of three groups (measured faster than six on MI355X: the
-    // first groups' compute starts sooner).
-    constexpr int FB = 3;
-    uint2 c[2][FB];
-    uint32_t sc[2][FB];
-    const bool whole = groups % (GEMV_WAVES * 2 * FB) == 0;
-    auto load_batch = [&](int b, int g) {
-        if (whole && g >= g_end) return;
-#pragma unroll
-        for (int u = 0; u < FB; ++u) {
-            if (whole || g + u < g_end) {
-                const v2u t =
-                    __builtin_nontemporal_load(reinterpret_cast<const v2u *>(cp + static_cast<size_t>(g + u) * 512));
-                c[b][u] = uint2{t[0], t[1]};
-                sc[b][u] = __builtin_nontemporal_load(sp + static_cast<size_t>(g + u) * 16);
-            }
-        }
-    };
-    load_batch(0, g_begin);
-    load_batch(1, g_begin + FB);
-
-    const int chunks = M * k / 8;  // 16-byte chunks of x
-    for (int i = threadIdx.x; i < chunks; i += GEMV_WAVES * WAVE)
-        reinterpret_cast<uint4 *>(xs_lds)[i] = reinterpret_cast<const uint4 *>(x)[i];
-    __syncthreads();
-    // xsum[row][4 g + q] = sum of the row's inputs 64 g + 8q .. +7 and
-    // 64 g + 32 + 8q .. +7 (the 16 inputs a lane with that q reads).
-    for (int i = threadIdx.x; i < M * groups * 4; i += GEMV_WAVES * WAVE) {
-        const int row = i / (groups * 4), gq = i % (groups * 4), g = gq >> 2, qq = gq & 3;
-        const uint16_t *xr = xs_lds + static_cast<size_t>(row) * k + g * 64 + 8 * qq;
-        float t = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) t += h2f(xr[e]) + h2f(xr[32 + e]);
-        xsum[i] = t;
-    }
-    __syncthreads();
+    const int per_wave = (groups + W - 1) / W;
+    const int g_begin = min(groups, wave * per_wave), g_end = min(groups, g_begin + per_wave);
+    const uint8_t *cp = codes + static_cast<size_t>(tile) * groups * 512 + h * 512 + j * 16;
+    const uint32_t *sp = reinterpret_cast<const uint32_t *>(scales) + static_cast<size_t>(tile) * groups * 16 + h * 16 + r0;
+    uint16_t *xw = xs[wave];
 
     uint32_t magic = 0x64006400u;
     asm volatile("" : "+v"(magic));  // kept in a VGPR: lets the insert be one v_bfi_b32
-    float yacc[M];
+    const v2h one2 = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+    float ya[M], yb[M];
 #pragma unroll
-    for (int r = 0; r < M; ++r) yacc[r] = 0.f;
-    auto consume = [&](int g, uint2 cc, uint32_t scq) {
-        v2h a[8];
+    for (int r = 0; r < M; ++r) ya[r] = yb[r] = 0.f;
+
+    for (int gc = g_begin; gc < g_end; gc += FB) {
+        // x slice: row r, groups gc .. gc + FB - 1 (clamped to the last group;
+        // clamped groups are never used).  Indices past the slice repeat its
+        // last chunk, so the loads and stores need no branch.
+        uint4 xv[XR];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            a[i] = __builtin_bit_cast(v2h, ((cc.x >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu));
-            a[4 + i] = __builtin_bit_cast(v2h, ((cc.y >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu));
+        for (int e = 0; e < XR; ++e) {
+            const int i = min(lane + e * WAVE, XC - 1), r = i / (FB * 8), cc = i % (FB * 8);
+            const int g = min(gc + (cc >> 3), groups - 1);
+            xv[e] = *reinterpret_cast<const uint4 *>(x + static_cast<size_t>(r) * k + g * 64 + (cc & 7) * 8);
         }
-        const float sc_s = h2f(static_cast<uint16_t>(scq & 0xFFFFu)), sc_m = h2f(static_cast<uint16_t>(scq >> 16));
+        v4u c[NI];
+        v2u sc[NI];
 #pragma unroll
-        for (int r = 0; r < M; ++r) {
-            const uint16_t *xr = xs_lds + static_cast<size_t>(r) * k + g * 64 + 8 * q;
-            const uint4 x0 = *reinterpret_cast<const uint4 *>(xr);
-            const uint4 x1 = *reinterpret_cast<const uint4 *>(xr + 32);
-            const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            float pl = 0.f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) pl = __builtin_amdgcn_fdot2(a[i], __builtin_bit_cast(v2h, xw[i]), pl, false);
-            const float xl = xsum[(r * groups + g) * 4 + q];
-            yacc[r] = __builtin_fmaf(sc_m, xl, yacc[r]);
-            yacc[r] = __builtin_fmaf(sc_s, __builtin_fmaf(-1024.0f, xl, pl), yacc[r]);
+        for (int u = 0; u < NI; ++u) {
+            const int g = min(gc + 2 * u, g_end - 1 - h);  // lane group gc + 2u + h, clamped into the wave's range
+            c[u] = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(cp + static_cast<size_t>(g) * 512));
+            sc[u] = __builtin_nontemporal_load(reinterpret_cast<const v2u *>(sp + static_cast<size_t>(g) * 16));
         }
-    };
-    for (int g = g_begin; g < g_end; g += 2 * FB) {
 #pragma unroll
-        for (int u = 0; u < FB; ++u)
-            if (whole || g + u < g_end) consume(g + u, c[0][u], sc[0][u]);
-        load_batch(0, g + 2 * FB);
+        for (int e = 0; e < XR; ++e) {
+            const int i = min(lane + e * WAVE, XC - 1);
+            reinterpret_cast<uint4 *>(xw)[i] = xv[e];
+        }
+        // The slice is the wave's own: its LDS stores are complete once
+        // lgkmcnt drains, and the wave barrier keeps the reads after them.
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int u = 0; u < FB; ++u)
-            if (whole || g + FB + u < g_end) consume(g + FB + u, c[1][u], sc[1][u]);
-        load_batch(1, g + 3 * FB);
+        for (int u = 0; u < NI; ++u) {
+            v2h a[8], b[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                a[i] = __builtin_bit_cast(v2h, ((c[u][0] >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu));
+                a[4 + i] = __builtin_bit_cast(v2h, ((c[u][1] >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu));
+                b[i] = __builtin_bit_cast(v2h, ((c[u][2] >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu));
+                b[4 + i] = __builtin_bit_cast(v2h, ((c[u][3] >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu));
+            }
+            // A group past the wave's range contributes nothing: its scale
+            // and minimum are taken as zero (selected here, where the loads
+            // are awaited anyway).
+            const v2u su = gc + 2 * u + h < g_end ? sc[u] : v2u{0u, 0u};
+            const float sa = h2f(static_cast<uint16_t>(su[0] & 0xFFFFu)), ma = h2f(static_cast<uint16_t>(su[0] >> 16));
+            const float sb = h2f(static_cast<uint16_t>(su[1] & 0xFFFFu)), mb = h2f(static_cast<uint16_t>(su[1] >> 16));
+#pragma unroll
+            for (int r = 0; r < M; ++r) {
+                const uint16_t *xr = xw + (r * FB + 2 * u + h) * 64 + 8 * q;
+                const uint4 x0 = *reinterpret_cast<const uint4 *>(xr);
+                const uint4 x1 = *reinterpret_cast<const uint4 *>(xr + 32);
+                const uint32_t xwd[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                float pa = 0.f, pb = 0.f, xl = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const v2h xq = __builtin_bit_cast(v2h, xwd[i]);
+                    pa = __builtin_amdgcn_fdot2(a[i], xq, pa, false);
+                    pb = __builtin_amdgcn_fdot2(b[i], xq, pb, false);
+                    xl = __builtin_amdgcn_fdot2(one2, xq, xl, false);
+                }
+                ya[r] = __builtin_fmaf(ma, xl, __builtin_fmaf(sa, __builtin_fmaf(-1024.0f, xl, pa), ya[r]));
+                yb[r] = __builtin_fmaf(mb, xl, __builtin_fmaf(sb, __builtin_fmaf(-1024.0f, xl, pb), yb[r]));
+            }
+        }
     }
 
-    // Sum the four lanes of a row (l, l + 16, l + 32, l + 48), then the waves.
+    // Lane bit 3 by a DPP row rotate of 8; bits 4..5 and the waves via LDS.
 #pragma unroll
     for (int r = 0; r < M; ++r) {
-        const float v = wave_sum16(yacc[r]);
-        if (q == 0) partial[wave][r][r16] = v;
+        const float va =
+            ya[r] + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, ya[r]), 0x128, 0xF,
+                                                                          0xF, false));
+        const float vb =
+            yb[r] + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, yb[r]), 0x128, 0xF,
+                                                                          0xF, false));
+        if ((lane & 8) == 0) {
+            partial[wave][lane >> 4][r][r0] = va;
+            partial[wave][lane >> 4][r][r0 + 1] = vb;
+        }
     }
     __syncthreads();
     if (threadIdx.x < M * 16) {
         const int r = threadIdx.x >> 4, nn = threadIdx.x & 15;
-        float v = partial[0][r][nn];
+        float v = 0.f;
 #pragma unroll
-        for (int w = 1; w < GEMV_WAVES; ++w) v += partial[w][r][nn];
+        for (int w = 0; w < W; ++w)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) v += partial[w][s][r][nn];
         const int col = tile * 16 + nn;
         store_out(y, static_cast<size_t>(r) * n + col, epilogue(v, bias, col, epi), out_type);
     }
@@ -385,14 +403,11 @@ static void launch_gemv(const uint16_t *x, const uint8_t *c, const uint16_t *s, 
                         int out_type, int epi, int m, int n, int k, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(n / 16)), block(GEMV_WAVES * WAVE);
     const long long lds = static_cast<long long>(m) * k * 2;
-    // One or two rows: the vector-unit form (x and its 16-input sums in LDS).
-    const long long lds_dot2 = lds + static_cast<long long>(m) * (k / 16) * 4;
-    if (m == 1 && lds_dot2 <= GEMV_LDS_X)
-        w4a16_gemv_dot2_kernel<1><<<grid, block, static_cast<size_t>(lds_dot2), stream>>>(x, c, s, bias, y, out_type,
-                                                                                         epi, n, k);
-    else if (m == 2 && lds_dot2 <= GEMV_LDS_X)
-        w4a16_gemv_dot2_kernel<2><<<grid, block, static_cast<size_t>(lds_dot2), stream>>>(x, c, s, bias, y, out_type,
-                                                                                         epi, n, k);
+    // One or two rows: the vector-unit form (its LDS does not grow with k).
+    if (m == 1)
+        w4a16_gemv_dot2_kernel<1><<<grid, dim3(DOT2_WAVES * WAVE), 0, stream>>>(x, c, s, bias, y, out_type, epi, n, k);
+    else if (m == 2)
+        w4a16_gemv_dot2_kernel<2><<<grid, dim3(DOT2_WAVES * WAVE), 0, stream>>>(x, c, s, bias, y, out_type, epi, n, k);
     else if (lds <= GEMV_LDS_X)
         w4a16_gemv_factored_kernel<<<grid, block, static_cast<size_t>(lds), stream>>>(x, c, s, bias, y, out_type, epi,
                                                                                       m, n, k);

@@ -182,7 +182,10 @@ def test_w4a16_epilogue_f16_bias_gelu(dev, gelu):
     _close(got, oracle.half_to_f32(oracle.half_from_f32(v)))
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 18432, 3072), (2, 18432, 3072), (3, 64, 256), (16, 512, 3584 // 64 * 64)])
+# m = 1, 2 also at group counts that leave waves idle (1, 13 groups) or a
+# ragged last chunk (56, 100 groups over eight waves of six-group chunks).
+@pytest.mark.parametrize("m,n,k", [(1, 18432, 3072), (2, 18432, 3072), (3, 64, 256), (16, 512, 3584 // 64 * 64),
+                                   (1, 96, 64), (2, 160, 832), (1, 48, 6400), (2, 32, 3584)])
 def test_w4a16_gemv(dev, m, n, k):
     print(f"gemv m={m} n={n} k={k}", flush=True)
     import qwen_image_hip.ops as ops
