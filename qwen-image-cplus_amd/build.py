@@ -21,6 +21,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OUT_DIR = PKG / "qwen_image_hip"
 LIB = OUT_DIR / "libqwen_image_hip.so"
+CLI = OUT_DIR / "qi-quantize"  # the pack writer / verifier command (cli/qi_quantize.cpp)
 BUILD = PKG / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CXX = os.environ.get("CXX", "g++")
@@ -84,6 +85,17 @@ def build_library(jobs: int = 8) -> Path:
     return LIB
 
 
+def build_cli() -> Path:
+    """The qi-quantize command, linked against the library next to it."""
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    tmp = CLI.with_suffix(".tmp")
+    _run([CXX, *[f for f in CXX_FLAGS if f != "-fvisibility=hidden"], "-D__HIP_PLATFORM_AMD__",
+          f"-I{rocm}/include", str(PKG / "cli" / "qi_quantize.cpp"), "-o", str(tmp), f"-L{OUT_DIR}",
+          "-lqwen_image_hip", f"-L{rocm}/lib", "-lamdhip64", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{rocm}/lib"])
+    os.replace(tmp, CLI)
+    return CLI
+
+
 def build_oracle() -> Path:
     subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], check=True)
     return ROOT / "oracle" / "_build" / "libqi_oracle.so"
@@ -95,6 +107,7 @@ def main(argv=None) -> int:
     ap.add_argument("-j", type=int, default=8)
     args = ap.parse_args(argv)
     print("built", build_library(args.j))
+    print("built", build_cli())
     if not args.lib_only:
         print("built", build_oracle())
     return 0
