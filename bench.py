@@ -11,6 +11,7 @@ W4A16 weights (config 2), the same W4A4 pass on the int8 operand path and
 the M=1/M=2 modulation GEMV (config 4) are reported beside it.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-extra]
+    python bench.py --library-only   # calibration: hipBLASLt plain fp16 / int8 GEMMs, same shapes
     python bench.py --kernel-only    # the dominant GEMM x 20 + a 512 MiB copy,
                                      # the workload of the counter runs
 """
@@ -560,6 +561,33 @@ def cpu_baseline(budget_s=20.0):
                       f"{oracle.num_threads()} threads ({platform.processor() or platform.machine()})"}
 
 
+def bench_library(iters=50):
+    """Calibration, not the product: the vendor library's plain GEMMs
+    (torch.matmul fp16 and torch._int_mm int8 through hipBLASLt, no group
+    structure, no quantisation) at the block's image-stream shapes and the
+    dual-stream QKV shape, against the same peaks as this build's kernels."""
+    import torch
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(99)
+    shapes = [(4096, 3 * HIDDEN, HIDDEN), (4096, HIDDEN, HIDDEN), (4096, 4 * HIDDEN, HIDDEN),
+              (4096, HIDDEN, 4 * HIDDEN), (4352, 3 * HIDDEN, HIDDEN)]
+    out = {}
+    for m, n, k in shapes:
+        x = torch.randn((m, k), generator=g, device="cuda").half()
+        w = torch.randn((n, k), generator=g, device="cuda").half()
+        ms = time_fn(lambda: x @ w.t(), iters, 5)
+        a = torch.randint(-7, 8, (m, k), generator=g, device="cuda", dtype=torch.int8)
+        b = torch.randint(-7, 8, (n, k), generator=g, device="cuda", dtype=torch.int8)
+        ms8 = time_fn(lambda: torch._int_mm(a, b.t()), iters, 5)
+        ops = 2.0 * m * n * k
+        out[f"{m}x{n}x{k}"] = {
+            "fp16_us": round(ms * 1e3, 1), "fp16_frac": round(ops / (ms * 1e-3) / PEAK_FP16_FLOPS, 4),
+            "int8_us": round(ms8 * 1e3, 1), "int8_frac": round(ops / (ms8 * 1e-3) / PEAK_INT8_OPS, 4)}
+        del x, w, a, b
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -576,6 +604,8 @@ def main(argv=None) -> int:
     ap.add_argument("--kernel-only", action="store_true",
                     help="run only the dominant GEMM (20 launches) and a 512 MiB device copy (5 launches), "
                          "for hardware-counter runs")
+    ap.add_argument("--library-only", action="store_true",
+                    help="only the calibration: the vendor library's plain fp16 / int8 GEMMs at the block's shapes")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -591,6 +621,9 @@ def main(argv=None) -> int:
         return kernel_only()
     if args.stack_only:
         print(json.dumps(bench_stack()), flush=True)
+        return 0
+    if args.library_only:
+        print(json.dumps({"library_gemm": bench_library()}), flush=True)
         return 0
     log("packing W4A4 block weights (fp6 operands)")
     blk4 = Block(q.SCHEME_W4A4_H256, 1)
