@@ -16,7 +16,8 @@
 // r < causal_rows, else every key.
 //
 // Design.  One wave owns 32 queries of one head; a workgroup of eight waves
-// shares 64-key tiles of K (row-major) and V (transposed) staged in LDS.
+// shares 64-key tiles of K (row-major) and V (transposed) staged in two LDS
+// slots, every thread staging part of each tile, one barrier per tile.
 // Scores are formed transposed, S^T = K Q^T on v_mfma_f32_32x32x16_f16
 // (A = K from LDS, B = Q^T held in registers), so lane l holds 32 scores of
 // ONE query (l % 32): the row max and sum are lane-local plus one exchange
@@ -51,15 +52,28 @@ __global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_kernel(
     const float *__restrict__ q, const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     float *__restrict__ out, int queries, int keys, int heads, int query_offset, int causal_rows,
     const int *__restrict__ visible_keys) {
-    __shared__ __attribute__((aligned(16))) uint16_t k_lds[ATT_KT * ATT_KROW];
-    __shared__ __attribute__((aligned(16))) uint16_t vt_lds[ATT_HD * ATT_VROW];
+    __shared__ __attribute__((aligned(16))) uint16_t k_lds2[2][ATT_KT * ATT_KROW];
+    __shared__ __attribute__((aligned(16))) uint16_t vt_lds2[2][ATT_HD * ATT_VROW];
     __shared__ int wg_visible;
 
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
     const int h = lane >> 5, l32 = lane & 31;
-    const int head = blockIdx.y;
+    int head, qblk;
+    {
+        const int nqb = gridDim.x, nh = gridDim.y;
+        const int id = blockIdx.x + nqb * blockIdx.y, total = nqb * nh;
+        const int xcd = id % 8, slot = id / 8;
+        // The hardware hands workgroup `id` to XCD id % 8; XCD x takes the
+        // linear work items [x * per, (x + 1) * per) of head-major order, so
+        // one head's query blocks share an XCD's L2 (measured 2 % faster).
+        const int per = (total + 7) / 8;
+        int w = xcd * per + slot;
+        if (total % 8 != 0 || w >= total) w = id;  // uneven split: keep the plain order
+        head = w / nqb;
+        qblk = w % nqb;
+    }
     const int width = heads * ATT_HD;
-    const int qi = blockIdx.x * ATT_QB + wave * 32 + l32;  // this lane's query
+    const int qi = qblk * ATT_QB + wave * 32 + l32;  // this lane's query
     const bool q_ok = qi < queries;
     const int visible = q_ok ? min(att_visible(qi + query_offset, keys, causal_rows, visible_keys), keys) : 0;
 
@@ -104,11 +118,13 @@ __global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_kernel(
 #pragma unroll
     for (int s = 32; s > 0; s >>= 1) wmin = min(wmin, __shfl_xor(wmin, s, 64));
 
-    // Tile staging through registers, one tile ahead: K as 4 16-byte chunks
-    // per thread (row-major), V as one 8-key x 8-dim block per thread < 128
-    // (transposed into LDS with byte permutes).
+    // Tile staging through registers into the LDS slot not being read: K as
+    // 16-byte chunks per thread (row-major), V as a 2-key x 8-dim block per
+    // thread (every thread takes part; the two rows' halves are paired into
+    // the transposed tile with byte permutes, one dword per dim, keys fastest
+    // across lanes so the 32 lanes of a row write distinct banks).
     uint4 kn[ATT_KCH];
-    uint32_t vn[8][4];
+    uint32_t vn[2][4];
     auto load_tile = [&](int start) {
 #pragma unroll
         for (int i = 0; i < ATT_KCH; ++i) {
@@ -118,12 +134,12 @@ __global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_kernel(
                 kn[i] = *reinterpret_cast<const uint4 *>(k + static_cast<size_t>(start + key) * width +
                                                          head * ATT_HD + chunk * 8);
         }
-        if (tid < 128) {
-            const int kb = tid >> 4, db = tid & 15;
+        {
+            const int kp = tid & 31, db = tid >> 5;
 #pragma unroll
-            for (int r = 0; r < 8; ++r) {
+            for (int r = 0; r < 2; ++r) {
                 uint4 t = uint4{0u, 0u, 0u, 0u};
-                const int key = start + 8 * kb + r;
+                const int key = start + 2 * kp + r;
                 if (key < keys)
                     t = *reinterpret_cast<const uint4 *>(v + static_cast<size_t>(key) * width + head * ATT_HD + 8 * db);
                 vn[r][0] = t.x;
@@ -133,35 +149,38 @@ __global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_kernel(
             }
         }
     };
-    auto store_tile = [&]() {
+    auto store_tile = [&](int buf) {
+        uint16_t *k_lds = k_lds2[buf];
+        uint16_t *vt_lds = vt_lds2[buf];
 #pragma unroll
         for (int i = 0; i < ATT_KCH; ++i) {
             const int idx = tid + i * ATT_WAVES * WAVE, key = idx >> 4, chunk = idx & 15;
             *reinterpret_cast<uint4 *>(k_lds + key * ATT_KROW + chunk * 8) = kn[i];
         }
-        if (tid < 128) {
-            const int kb = tid >> 4, db = tid & 15;
+        {
+            const int kp = tid & 31, db = tid >> 5;
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
-                // dim 8db + c = half c % 2 of dword c / 2 of every row; the
-                // output dword e pairs rows 2e (low half) and 2e + 1.
                 const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
-                uint4 t;
-                t.x = __builtin_amdgcn_perm(vn[1][c >> 1], vn[0][c >> 1], sel);
-                t.y = __builtin_amdgcn_perm(vn[3][c >> 1], vn[2][c >> 1], sel);
-                t.z = __builtin_amdgcn_perm(vn[5][c >> 1], vn[4][c >> 1], sel);
-                t.w = __builtin_amdgcn_perm(vn[7][c >> 1], vn[6][c >> 1], sel);
-                *reinterpret_cast<uint4 *>(vt_lds + (8 * db + c) * ATT_VROW + 8 * kb) = t;
+                *reinterpret_cast<uint32_t *>(vt_lds + (8 * db + c) * ATT_VROW + 2 * kp) =
+                    __builtin_amdgcn_perm(vn[1][c >> 1], vn[0][c >> 1], sel);
             }
         }
     };
 
-    if (limit > 0) load_tile(0);
-    for (int start = 0; start < limit; start += ATT_KT) {
-        __syncthreads();  // the previous tile's readers are done
-        store_tile();
+    // Two LDS slots: tile i is read from slot i % 2 while tile i + 1 (loaded
+    // into registers during tile i - 1) is stored into the other after the
+    // tile's products; one barrier per tile then orders both.
+    if (limit > 0) {
+        load_tile(0);
+        store_tile(0);
         __syncthreads();
-        if (start + ATT_KT < limit) load_tile(start + ATT_KT);
+        if (ATT_KT < limit) load_tile(ATT_KT);
+    }
+    int buf = 0;
+    for (int start = 0; start < limit; start += ATT_KT, buf ^= 1) {
+        const uint16_t *k_lds = k_lds2[buf];
+        const uint16_t *vt_lds = vt_lds2[buf];
 
         // S^T for the tile's two 32-key halves t: register 4a + b of s[t]
         // holds key start + 32t + 8a + 4h + b of the lane's query.
@@ -228,6 +247,9 @@ __global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_kernel(
                     o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[t][e], o[j], 0, 0, 0);
                 }
         }
+        if (start + ATT_KT < limit) store_tile(buf ^ 1);
+        __syncthreads();
+        if (start + 2 * ATT_KT < limit) load_tile(start + 2 * ATT_KT);
     }
 
     // Both halves' sums, then O / sum (0 when nothing was visible).
