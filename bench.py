@@ -346,6 +346,34 @@ def bench_gemv(iters=200):
         total = bytes_per + m * k * 2 + m * n * 2
         out[f"m{m}"] = {"us": round(ms * 1e3, 3), "GB_s": round(total / (ms * 1e-3) / 1e9, 1),
                         "frac_hbm": round(total / (ms * 1e-3) / PEAK_HBM, 4), "bytes": total}
+
+    # Every block's modulation linears (60 blocks x image and text stream)
+    # read the same timestep embedding, so with all blocks resident they run
+    # as one GEMV over the stacked tiled weights (a fused record of 120
+    # parts, m = 1: one launch), against one launch per matrix.  The 120
+    # matrices are 8 packed random matrices repeated (distinct memory; the
+    # bytes read are what is timed).
+    parts = 120
+    reps = [pool[i % 8] for i in range(parts)]
+    codes_all = torch.cat([r.tiled_codes for r in reps], 0)
+    scales_all = torch.cat([r.tiled_scales for r in reps], 0)
+    del reps
+    x = torch.randn((1, k), generator=g, device="cuda").half()
+    y_all = torch.empty((1, parts * n), dtype=torch.float16, device="cuda")
+    ms_one = time_fn(lambda: ops.w4a16_gemv(x, codes_all, scales_all, out_dtype=torch.float16, y=y_all), 20, 3)
+
+    def per_matrix():
+        for p in range(parts):
+            ops.w4a16_gemv(x, codes_all[p * n:(p + 1) * n], scales_all[p * n:(p + 1) * n],
+                           out_dtype=torch.float16, y=y_all[:, p * n:(p + 1) * n])
+
+    ms_each = time_fn(per_matrix, 5, 1)
+    total = parts * bytes_per + k * 2 + parts * n * 2
+    out["m1_all_blocks"] = {"matrices": parts, "bytes": total, "one_launch_us": round(ms_one * 1e3, 1),
+                            "GB_s": round(total / (ms_one * 1e-3) / 1e9, 1),
+                            "frac_hbm": round(total / (ms_one * 1e-3) / PEAK_HBM, 4),
+                            "per_matrix_launches_us": round(ms_each * 1e3, 1)}
+    del codes_all, scales_all
     return out
 
 

@@ -713,6 +713,13 @@ QI_API int qi_hip_w4a16_gemm_tiled_parts(const void *x_half, const void *w_tiled
                                          int n_part, void *stream) {
     if (const int st = check_w4a16_args(x_half, w_tiled_codes, w_tiled_scales, y, out_type, epilogue, m, n, k, n_part))
         return st;
+    if (m == 1)
+        // One row: the parts layout [part][1][n_part] is the row-major
+        // [1][n] output, and the parts' tiles are consecutive, so one GEMV
+        // over all n covers every part (e.g. every block's modulation
+        // linears, which share their input, in one launch).
+        return qi_hip_w4a16_gemv_impl(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, 1, n, k,
+                                      stream_of(stream));
     if (m <= 16) {
         // One GEMV per part: a part is n_part / 16 whole weight tiles.
         const size_t tile_codes = static_cast<size_t>(k / 64) * 64 * 8, tile_scales = static_cast<size_t>(k / 64) * 64;

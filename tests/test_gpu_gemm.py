@@ -340,11 +340,11 @@ def test_linear_from_qipack_file(dev, tmp_path, scheme):
     np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-@pytest.mark.parametrize("m", [2, 300, 4096])
+@pytest.mark.parametrize("m", [1, 2, 300, 4096])
 def test_w4a16_fused_record_matches_separate_records(dev, m):
     """A fused (q, k, v) W4A16 record: each part within the W4A16 tolerance of
     the part's own call, and bit-identical on the GEMV path (m <= 16), which
-    runs the same kernel per part."""
+    runs the same kernel per part (m = 1: one launch over all parts)."""
     import qwen_image_hip as q
     n, k = 1024, 640
     print(f"w4a16 fused qkv m={m} n={n} k={k}", flush=True)
