@@ -373,6 +373,13 @@ def bench_gemv(iters=200):
                             "GB_s": round(total / (ms_one * 1e-3) / 1e9, 1),
                             "frac_hbm": round(total / (ms_one * 1e-3) / PEAK_HBM, 4),
                             "per_matrix_launches_us": round(ms_each * 1e3, 1)}
+    x2 = torch.randn((2, k), generator=g, device="cuda").half()
+    y2 = torch.empty((2, parts * n), dtype=torch.float16, device="cuda")
+    ms_two = time_fn(lambda: ops.w4a16_gemv(x2, codes_all, scales_all, out_dtype=torch.float16, y=y2), 20, 3)
+    total2 = parts * bytes_per + 2 * k * 2 + 2 * parts * n * 2
+    out["m2_all_blocks"] = {"matrices": parts, "bytes": total2, "one_launch_us": round(ms_two * 1e3, 1),
+                            "GB_s": round(total2 / (ms_two * 1e-3) / 1e9, 1),
+                            "frac_hbm": round(total2 / (ms_two * 1e-3) / PEAK_HBM, 4)}
     del codes_all, scales_all
     return out
 

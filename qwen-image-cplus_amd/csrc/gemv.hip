@@ -30,12 +30,20 @@ constexpr int GEMV_WAVES = 4;
 constexpr int GEMV_BATCH = 4;  // groups per batch; two batches are in flight per wave
 constexpr int GEMV_LDS_X = 48 * 1024;  // bytes of activations staged in LDS
 
+// Output index of row r, column col: the parts layout [part][m][n_part]
+// (n_part = n: the row-major [m][n]).  n_part is a multiple of 16, so a
+// workgroup's 16 columns lie in one part.
+__device__ __forceinline__ size_t gemv_out_index(int r, int col, int m, int n_part) {
+    const int part = col / n_part;
+    return (static_cast<size_t>(part) * m + r) * n_part + (col - part * n_part);
+}
+
 // XLDS: the workgroup first copies x (m rows x k fp16) into LDS, so the
 // weight stream never waits on activation loads; used when m * k * 2 fits.
 template <bool XLDS>
 __global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
-    const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int m, int n, int k) {
+    const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int m, int n, int k, int n_part) {
     __shared__ float partial[GEMV_WAVES][16][17];
     extern __shared__ __attribute__((aligned(16))) uint16_t xs_lds[];  // m * k fp16 when XLDS
     const int groups = k >> 6;
@@ -120,7 +128,7 @@ __global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_kernel(
 #pragma unroll
             for (int w = 1; w < GEMV_WAVES; ++w) v += partial[w][nn][mm];
             const int col = tile * 16 + nn;
-            store_out(y, static_cast<size_t>(mm) * n + col, epilogue(v, bias, col, epi), out_type);
+            store_out(y, gemv_out_index(mm, col, m, n_part), epilogue(v, bias, col, epi), out_type);
         }
     }
 }
@@ -138,7 +146,7 @@ __global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_kernel(
 // the fp16 weight rounding only, well inside the W4A16 output tolerance.
 __global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_factored_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
-    const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int m, int n, int k) {
+    const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int m, int n, int k, int n_part) {
     __shared__ float partial[GEMV_WAVES][16][17];
     extern __shared__ __attribute__((aligned(16))) uint16_t xs_lds[];  // m * k fp16
     const int groups = k >> 6;
@@ -254,7 +262,7 @@ __global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_factored_kernel(
 #pragma unroll
             for (int w = 1; w < GEMV_WAVES; ++w) v += partial[w][nn][mm];
             const int col = tile * 16 + nn;
-            store_out(y, static_cast<size_t>(mm) * n + col, epilogue(v, bias, col, epi), out_type);
+            store_out(y, gemv_out_index(mm, col, m, n_part), epilogue(v, bias, col, epi), out_type);
         }
     }
 }
@@ -285,7 +293,7 @@ constexpr int DOT2_FB = 6;  // groups per wave and chunk: three 16-byte loads pe
 template <int M>
 __global__ __launch_bounds__(DOT2_WAVES *WAVE) void w4a16_gemv_dot2_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
-    const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int n, int k) {
+    const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int n, int k, int n_part) {
     constexpr int W = DOT2_WAVES, FB = DOT2_FB, NI = FB / 2;
     constexpr int XC = M * FB * 8;  // 16-byte chunks of a wave's x slice
     constexpr int XR = (XC + WAVE - 1) / WAVE;
@@ -395,24 +403,24 @@ __global__ __launch_bounds__(DOT2_WAVES *WAVE) void w4a16_gemv_dot2_kernel(
 #pragma unroll
             for (int s = 0; s < 4; ++s) v += partial[w][s][r][nn];
         const int col = tile * 16 + nn;
-        store_out(y, static_cast<size_t>(r) * n + col, epilogue(v, bias, col, epi), out_type);
+        store_out(y, gemv_out_index(r, col, M, n_part), epilogue(v, bias, col, epi), out_type);
     }
 }
 
 static void launch_gemv(const uint16_t *x, const uint8_t *c, const uint16_t *s, const float *bias, void *y,
-                        int out_type, int epi, int m, int n, int k, hipStream_t stream) {
+                        int out_type, int epi, int m, int n, int k, int n_part, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(n / 16)), block(GEMV_WAVES * WAVE);
     const long long lds = static_cast<long long>(m) * k * 2;
     // One or two rows: the vector-unit form (its LDS does not grow with k).
     if (m == 1)
-        w4a16_gemv_dot2_kernel<1><<<grid, dim3(DOT2_WAVES * WAVE), 0, stream>>>(x, c, s, bias, y, out_type, epi, n, k);
+        w4a16_gemv_dot2_kernel<1><<<grid, dim3(DOT2_WAVES * WAVE), 0, stream>>>(x, c, s, bias, y, out_type, epi, n, k, n_part);
     else if (m == 2)
-        w4a16_gemv_dot2_kernel<2><<<grid, dim3(DOT2_WAVES * WAVE), 0, stream>>>(x, c, s, bias, y, out_type, epi, n, k);
+        w4a16_gemv_dot2_kernel<2><<<grid, dim3(DOT2_WAVES * WAVE), 0, stream>>>(x, c, s, bias, y, out_type, epi, n, k, n_part);
     else if (lds <= GEMV_LDS_X)
         w4a16_gemv_factored_kernel<<<grid, block, static_cast<size_t>(lds), stream>>>(x, c, s, bias, y, out_type, epi,
-                                                                                      m, n, k);
+                                                                                      m, n, k, n_part);
     else
-        w4a16_gemv_kernel<false><<<grid, block, 0, stream>>>(x, c, s, bias, y, out_type, epi, m, n, k);
+        w4a16_gemv_kernel<false><<<grid, block, 0, stream>>>(x, c, s, bias, y, out_type, epi, m, n, k, n_part);
 }
 
 }  // namespace qi
@@ -420,12 +428,12 @@ static void launch_gemv(const uint16_t *x, const uint8_t *c, const uint16_t *s, 
 using namespace qi;
 
 int qi_hip_w4a16_gemv_impl(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
-                           const float *bias, void *y, int out_type, int epilogue, int m, int n, int k,
+                           const float *bias, void *y, int out_type, int epilogue, int m, int n, int k, int n_part,
                            hipStream_t stream) {
     const uint16_t *x = static_cast<const uint16_t *>(x_half);
     const uint8_t *c = static_cast<const uint8_t *>(w_tiled_codes);
     const uint16_t *s = static_cast<const uint16_t *>(w_tiled_scales);
-    launch_gemv(x, c, s, bias, y, out_type, epilogue, m, n, k, stream);
+    launch_gemv(x, c, s, bias, y, out_type, epilogue, m, n, k, n_part, stream);
     return launch_status();
 }
 
@@ -439,6 +447,6 @@ QI_API int qi_hip_w4a16_gemv(const void *x_half, const void *w_tiled_codes, cons
     if (reinterpret_cast<uintptr_t>(x_half) % 16 || reinterpret_cast<uintptr_t>(w_tiled_codes) % 8 ||
         reinterpret_cast<uintptr_t>(w_tiled_scales) % 4)
         return kInvalid;
-    return qi_hip_w4a16_gemv_impl(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
+    return qi_hip_w4a16_gemv_impl(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k, n,
                                   stream_of(stream));
 }

@@ -599,7 +599,7 @@ static int dispatch(const void *x, const void *codes, const void *scales, const 
 using namespace qi;
 
 int qi_hip_w4a16_gemv_impl(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
-                           const float *bias, void *y, int out_type, int epilogue, int m, int n, int k,
+                           const float *bias, void *y, int out_type, int epilogue, int m, int n, int k, int n_part,
                            hipStream_t stream);
 
 QI_API int qi_w4a16_gemm(const void *x_half, const void *codes, const void *scales, const void *minimums, float *y,
@@ -713,27 +713,11 @@ QI_API int qi_hip_w4a16_gemm_tiled_parts(const void *x_half, const void *w_tiled
                                          int n_part, void *stream) {
     if (const int st = check_w4a16_args(x_half, w_tiled_codes, w_tiled_scales, y, out_type, epilogue, m, n, k, n_part))
         return st;
-    if (m == 1)
-        // One row: the parts layout [part][1][n_part] is the row-major
-        // [1][n] output, and the parts' tiles are consecutive, so one GEMV
-        // over all n covers every part (e.g. every block's modulation
-        // linears, which share their input, in one launch).
-        return qi_hip_w4a16_gemv_impl(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, 1, n, k,
-                                      stream_of(stream));
-    if (m <= 16) {
-        // One GEMV per part: a part is n_part / 16 whole weight tiles.
-        const size_t tile_codes = static_cast<size_t>(k / 64) * 64 * 8, tile_scales = static_cast<size_t>(k / 64) * 64;
-        const size_t out_bytes = static_cast<size_t>(m) * n_part * (out_type == QI_HIP_OUT_F16 ? 2 : 4);
-        for (int p = 0; p < n / n_part; ++p) {
-            const size_t tiles = static_cast<size_t>(p) * (n_part / 16);
-            const int st = qi_hip_w4a16_gemv_impl(
-                x_half, static_cast<const uint8_t *>(w_tiled_codes) + tiles * tile_codes,
-                static_cast<const uint8_t *>(w_tiled_scales) + tiles * tile_scales, bias ? bias + p * n_part : nullptr,
-                static_cast<uint8_t *>(y) + p * out_bytes, out_type, epilogue, m, n_part, k, stream_of(stream));
-            if (st) return st;
-        }
-        return 0;
-    }
+    if (m <= 16)
+        // The GEMV writes the parts layout itself: one launch over all parts
+        // (e.g. every block's modulation linears, which share their input).
+        return qi_hip_w4a16_gemv_impl(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
+                                      n_part, stream_of(stream));
     if (static_cast<long long>(m) * k * 2 >= (1LL << 32) || static_cast<long long>(n) * (k / 2) >= (1LL << 32))
         return kInvalid;
     return dispatch_w4a16(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k, n_part,

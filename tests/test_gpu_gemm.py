@@ -340,13 +340,16 @@ def test_linear_from_qipack_file(dev, tmp_path, scheme):
     np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-@pytest.mark.parametrize("m", [1, 2, 300, 4096])
-def test_w4a16_fused_record_matches_separate_records(dev, m):
+# m = 1, 2: the vector-unit GEMV; 5: the factored matrix-core GEMV; 16 at
+# k = 2048: the dequantising GEMV (x too large for LDS).
+@pytest.mark.parametrize("m,k", [(1, 640), (2, 640), (5, 640), (16, 2048), (300, 640), (4096, 640)])
+def test_w4a16_fused_record_matches_separate_records(dev, m, k):
     """A fused (q, k, v) W4A16 record: each part within the W4A16 tolerance of
     the part's own call, and bit-identical on the GEMV path (m <= 16), which
-    runs the same kernel per part (m = 1: one launch over all parts)."""
+    runs the same kernel as the part's own call in one launch over all parts,
+    writing the parts layout."""
     import qwen_image_hip as q
-    n, k = 1024, 640
+    n = 1024
     print(f"w4a16 fused qkv m={m} n={n} k={k}", flush=True)
     x = _h(f16_bits(normal_f32(m, k, 730 + m)), dev)
     recs = [q.PackedLinear.from_fp16(q.SCHEME_W4A16, _h(weights_f16(n, k, 731 + i), dev)) for i in range(3)]
