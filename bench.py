@@ -14,6 +14,8 @@ the M=1/M=2 modulation GEMV (config 4) are reported beside it.
     python bench.py --library-only   # calibration: hipBLASLt plain fp16 / int8 GEMMs, same shapes
     python bench.py --kernel-only    # the dominant GEMM x 20 + a 512 MiB copy,
                                      # the workload of the counter runs
+    python bench.py --gemv-only      # the all-blocks modulation GEMV x 10 + a
+                                     # 512 MiB copy, for the GEMV's counter runs
 """
 from __future__ import annotations
 
@@ -303,6 +305,41 @@ def kernel_only():
         dst.copy_(src)
     torch.cuda.synchronize()
     log("kernel-only: 20 x dual-stream w4a4 GEMM (4096+256)x(2x9216)x3072 (fused qkv), 5 x copy 536870912 B")
+    return 0
+
+
+def gemv_only():
+    """The HBM-bound kernel's counter workload: all 60 blocks' modulation
+    linears (image + text stream, 120 x 3072->18432, m = 1) as one fused GEMV
+    launch x 11 (the last 10 timed), then a plain 512 MiB copy x 5 whose known byte count
+    calibrates the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+    import qwen_image_hip as q
+    from qwen_image_hip import ops
+
+    n, k, parts = MODULATION_N, HIDDEN, 120
+    g = torch.Generator(device="cuda")
+    g.manual_seed(77)
+    pool = []
+    for _ in range(8):
+        w = (torch.randn((n, k), generator=g, device="cuda") * 0.02).half()
+        pool.append(q.PackedLinear.from_fp16(q.SCHEME_W4A16, w))
+        del w
+    codes_all = torch.cat([pool[i % 8].tiled_codes for i in range(parts)], 0)
+    scales_all = torch.cat([pool[i % 8].tiled_scales for i in range(parts)], 0)
+    del pool
+    x = torch.randn((1, k), generator=g, device="cuda").half()
+    y = torch.empty((1, parts * n), dtype=torch.float16, device="cuda")
+    ops.w4a16_gemv(x, codes_all, scales_all, out_dtype=torch.float16, y=y)
+    ms = time_fn(lambda: ops.w4a16_gemv(x, codes_all, scales_all, out_dtype=torch.float16, y=y), 10, 0)
+    src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    total = parts * (n * k // 2 + n * (k // 64) * 4) + k * 2 + parts * n * 2
+    log(f"gemv-only: 1 + 10 x fused modulation GEMV m=1 n={parts}x{n} k={k} ({total} algorithmic bytes), "
+        f"{ms * 1e3:.1f} us per launch by HIP events over the 10; 5 x copy 536870912 B")
     return 0
 
 
@@ -639,6 +676,9 @@ def main(argv=None) -> int:
     ap.add_argument("--kernel-only", action="store_true",
                     help="run only the dominant GEMM (20 launches) and a 512 MiB device copy (5 launches), "
                          "for hardware-counter runs")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="run only the all-blocks modulation GEMV (11 launches) and a 512 MiB device copy "
+                         "(5 launches), for hardware-counter runs")
     ap.add_argument("--library-only", action="store_true",
                     help="only the calibration: the vendor library's plain fp16 / int8 GEMMs at the block's shapes")
     args = ap.parse_args(argv)
@@ -654,6 +694,8 @@ def main(argv=None) -> int:
     torch.cuda.set_device(0)
     if args.kernel_only:
         return kernel_only()
+    if args.gemv_only:
+        return gemv_only()
     if args.stack_only:
         print(json.dumps(bench_stack()), flush=True)
         return 0
