@@ -16,6 +16,7 @@ the M=1/M=2 modulation GEMV (config 4) are reported beside it.
                                      # the workload of the counter runs
     python bench.py --gemv-only      # the all-blocks modulation GEMV x 10 + a
                                      # 512 MiB copy, for the GEMV's counter runs
+    python bench.py --w4a16-only     # the W4A16 MLP-up GEMM x 11 + a 512 MiB copy
 """
 from __future__ import annotations
 
@@ -239,6 +240,27 @@ class StepW4A16:
         ops.w4a16_gemm_dual(b["h"], r.tiled_codes, r.tiled_scales, split, out_dtype=f16, y=b["y"])
 
 
+def device_peaks():
+    """The box's own peaks: reported CU count x peak engine clock x per-CU
+    dense rate (gfx950: 8192 int8 ops, 4096 fp16 flops per CU per clock),
+    beside the published figures the roofline fractions use."""
+    import ctypes
+
+    import torch
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    clock_khz, cus = ctypes.c_int(0), ctypes.c_int(0)
+    # hipDeviceAttributeClockRate = 5, hipDeviceAttributeMultiprocessorCount = 63 (hip_runtime_api.h).
+    if hip.hipDeviceGetAttribute(ctypes.byref(clock_khz), 5, 0) or hip.hipDeviceGetAttribute(ctypes.byref(cus), 63, 0):
+        return None
+    hz = clock_khz.value * 1e3
+    return {"cus": cus.value, "peak_sclk_mhz": round(hz / 1e6), "name": torch.cuda.get_device_properties(0).name,
+            "int8_tops_at_clock": round(cus.value * hz * 8192 / 1e12, 1),
+            "fp16_tflops_at_clock": round(cus.value * hz * 4096 / 1e12, 1),
+            "int8_tops_published": PEAK_INT8_OPS / 1e12, "fp16_tflops_published": PEAK_FP16_FLOPS / 1e12,
+            "hbm_gb_s_published": PEAK_HBM / 1e9}
+
+
 def time_fn(fn, iters, warmup):
     """Mean ms per call with HIP events on the current stream (the one every
     op is launched on)."""
@@ -340,6 +362,39 @@ def gemv_only():
     total = parts * (n * k // 2 + n * (k // 64) * 4) + k * 2 + parts * n * 2
     log(f"gemv-only: 1 + 10 x fused modulation GEMV m=1 n={parts}x{n} k={k} ({total} algorithmic bytes), "
         f"{ms * 1e3:.1f} us per launch by HIP events over the 10; 5 x copy 536870912 B")
+    return 0
+
+
+def w4a16_only():
+    """The fp16-MFMA kernel's counter workload: the image stream's W4A16 MLP
+    up linear (4096 x 12288 x 3072, GELU-tanh, fp16 out) x 11 (the last 10
+    timed), then a plain 512 MiB copy x 5 for the counter calibration."""
+    import torch
+    import qwen_image_hip as q
+    from qwen_image_hip import ops
+
+    m, n, k = STREAMS["image"], MLP, HIDDEN
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    w = (torch.randn((n, k), generator=g, device="cuda") * 0.02).half()
+    rec = q.PackedLinear.from_fp16(q.SCHEME_W4A16, w)
+    del w
+    x = torch.randn((m, k), generator=g, device="cuda").half()
+    y = torch.empty((m, n), dtype=torch.float16, device="cuda")
+
+    def fn():
+        ops.w4a16_gemm(x, rec.tiled_codes, rec.tiled_scales, out_dtype=torch.float16, gelu=True, y=y)
+
+    fn()
+    ms = time_fn(fn, 10, 0)
+    src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    total = n * k // 2 + n * (k // 64) * 4 + m * k * 2 + m * n * 2
+    log(f"w4a16-only: 1 + 10 x W4A16 GEMM m={m} n={n} k={k} gelu fp16 out ({total} algorithmic bytes, "
+        f"{2 * m * n * k} flops), {ms * 1e3:.1f} us per launch by HIP events over the 10; 5 x copy 536870912 B")
     return 0
 
 
@@ -679,6 +734,9 @@ def main(argv=None) -> int:
     ap.add_argument("--gemv-only", action="store_true",
                     help="run only the all-blocks modulation GEMV (11 launches) and a 512 MiB device copy "
                          "(5 launches), for hardware-counter runs")
+    ap.add_argument("--w4a16-only", action="store_true",
+                    help="run only the W4A16 MLP-up GEMM (11 launches) and a 512 MiB device copy (5 launches), "
+                         "for hardware-counter runs")
     ap.add_argument("--library-only", action="store_true",
                     help="only the calibration: the vendor library's plain fp16 / int8 GEMMs at the block's shapes")
     args = ap.parse_args(argv)
@@ -696,6 +754,8 @@ def main(argv=None) -> int:
         return kernel_only()
     if args.gemv_only:
         return gemv_only()
+    if args.w4a16_only:
+        return w4a16_only()
     if args.stack_only:
         print(json.dumps(bench_stack()), flush=True)
         return 0
@@ -810,6 +870,7 @@ def main(argv=None) -> int:
                    "global_batch": 1, "seq_len": sum(STREAMS.values()), "parallelism": "single-gpu", "streams": 2 if args.two_streams else 1},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "peaks": device_peaks(),
     }
     line.update(extra)
     print(json.dumps(line), flush=True)
