@@ -626,13 +626,14 @@ static int dispatch_w4a16(const void *x, const void *codes, const void *scales, 
                           hipStream_t s) {
     const int n_out = out.n_out;
     // QI_HIP_W4A16_TILES forces a shape, for tuning: 1 K-split 64 x 64, 2
-    // tiled 32 x 64, 3 tiled 64 x 64, 4 tiled 128 x 192.
+    // tiled 32 x 64, 3 tiled 64 x 64, 4 tiled 128 x 192, 5 tiled 256 x 256, 6 tiled
+    // 128 x 128.
     static const int forced = [] {
         const char *e = getenv("QI_HIP_W4A16_TILES");
         return e ? atoi(e) : -1;
     }();
     int cfg;  // 1 K-split, 2..4 as above, 5 tiled 256 x 256, 6 tiled 128 x 128
-    if (forced >= 1 && forced <= 4 && (forced != 4 || n_out % 192 == 0))
+    if (forced >= 1 && forced <= 6 && (forced != 4 || n_out % 192 == 0) && (forced != 5 || n_out % 256 == 0))
         cfg = forced;
     // Short M with few column tiles (the text stream's 256 x 3072 outputs):
     // the tiled grid is too small to fill the chip, so split K across the
@@ -642,7 +643,12 @@ static int dispatch_w4a16(const void *x, const void *codes, const void *scales, 
         cfg = 1;
     else if (m <= 256)
         cfg = 2;  // short row tiles so the grid still covers the 256 CUs
-    else if (m <= 1024)
+    // 128 x 192 tiles once they make three quarters of a round of
+    // workgroups (two per CU) or more, else 64 x 64 tiles (measured:
+    // 1024 x 12288 x 3072 123.5 -> 98.4 us with 512 large tiles; 1536 x 3072
+    // x 3072 with 192 large tiles 74.7 us against 63.9 for small ones).
+    else if (!(n_out % 192 == 0 && static_cast<long long>((m + 127) / 128) * (n_out / 192) >= 384) &&
+             (m <= 1024 || n_out % 192 == 0))
         cfg = 3;
     // 256 x 256 tiles (eight waves, one workgroup per CU: each weight is
     // dequantised for twice the rows) when they still give three or more

@@ -135,9 +135,11 @@ def test_w4a16_reference_abi(dev, m, n, k):
 # m <= 256 with few column tiles runs the K-split kernel (17, 100, 256
 # rows here), larger m the tiled kernel.  The M = 300 rows are the
 # text-encoder shapes of config 4 (Qwen2.5-VL-7B: hidden 3584, MLP 18944).
+# 600 x 18432 runs the 128 x 192 tiles on a ragged last row band.
 @pytest.mark.parametrize("m,n,k,clip", [(17, 16, 64, False), (100, 48, 192, True), (256, 192, 3072, False),
                                         (300, 512, 3584 // 64 * 64, False), (1024, 256, 1024, True),
-                                        (300, 2048, 3584, False), (300, 1024, 18944, False)])
+                                        (300, 2048, 3584, False), (300, 1024, 18944, False),
+                                        (600, 18432, 256, False)])
 def test_w4a16_tiled(dev, m, n, k, clip):
     print(f"w4a16 tiled m={m} n={n} k={k}", flush=True)
     import qwen_image_hip.ops as ops
