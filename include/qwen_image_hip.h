@@ -46,7 +46,7 @@ extern "C" {
 #endif
 
 /* ABI version of this header; bumped on any signature change. */
-#define QI_HIP_ABI_VERSION 2
+#define QI_HIP_ABI_VERSION 3
 int qi_hip_abi_version(void);
 
 /* ---------------------------------------------------------------------------
@@ -149,6 +149,14 @@ int qi_hip_w4a16_gemm_tiled_dual(const void *x_half, const void *w_tiled_codes, 
                                  const float *bias, void *y, int out_type, int epilogue, int m, int m_split, int n,
                                  int k, int n_part, void *stream);
 
+/* The kernel shape the W4A16 GEMMs above choose for m rows and n_out
+ * outputs per stream: 0 GEMV (m <= 16), 1 K-split 64 x 64 tiles, 2 tiled
+ * 32 x 64, 3 tiled 64 x 64, 4 tiled 128 x 192, 5 tiled 256 x 256, 6 tiled
+ * 128 x 128; -1 for m or n_out <= 0.  A query only (tests and tuning): no
+ * device work.  No counterpart in the reference, whose one W4A16 kernel has
+ * a fixed tile (gemm.cu:191-268). */
+int qi_hip_w4a16_tiles(int m, int n_out);
+
 /* Bandwidth-bound W4A16 GEMV for 1 <= m <= 16 (the adaLN / timestep
  * modulation linears).  Same arithmetic and layouts as above.  The
  * reference runs these linears as BF16 -> fp32 SGEMM
@@ -189,6 +197,12 @@ int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *w_codes6, const float
  * output is bit-identical to the per-record call's. */
 int qi_hip_w4a4_gemm_fp6_parts(const void *a_codes6, const void *w_codes6, const float *bias, void *y,
                                int out_type, int epilogue, int m, int n, int k, int n_part, void *stream);
+/* The tile shape qi_hip_w4a4_gemm_fp6[_parts] chooses for m rows and n
+ * outputs: 0 = 128 x 128 tiles, one per workgroup; 1 = the same tiles walked
+ * by the persistent kernel (m, n multiples of 128); 3 = 64 x 128 tiles; 4 =
+ * single-wave 32 x 32 tiles; -1 for m or n <= 0.  A query only: no device
+ * work.  No counterpart in the reference (fixed tile, gemm.cu:59-189). */
+int qi_hip_w4a4_fp6_tiles(int m, int n);
 /* Both streams of an MMDiT dual-stream block in one call (the reference
  * runs the image and the text stream's linear as two
  * transformer::linear calls on their own rows).  a_codes6: m rows of fp6

@@ -16,7 +16,6 @@
 // double-buffered so one barrier per group suffices, and the next group's
 // codes, scales and activations are loaded while the current group computes.
 
-#include <cstdlib>
 
 #include "qi_common.h"
 
@@ -615,6 +614,31 @@ QI_API int qi_w4a16_gemm(const void *x_half, const void *codes, const void *scal
 
 namespace qi {
 
+// Kernel shape for m > 16 rows and n_out outputs per stream (measured on
+// MI355X): 1 K-split 64 x 64, 2 tiled 32 x 64, 3 tiled 64 x 64, 4 tiled
+// 128 x 192, 5 tiled 256 x 256, 6 tiled 128 x 128.
+static int select_w4a16_tiles(int m, int n_out) {
+    // Short M with few column tiles (the text stream's 256 x 3072 outputs):
+    // the tiled grid is too small to fill the chip, so split K across the
+    // workgroup's waves instead (measured: 256 x 3072 x 3072 20.4 -> 17.5 us,
+    // 256 x 3072 x 12288 67.4 -> 49.3 us; wider N keeps the tiled kernel).
+    if (m <= 256 && static_cast<long long>((m + 31) / 32) * ((n_out + 63) / 64) < 1024) return 1;
+    if (m <= 256) return 2;  // short row tiles so the grid still covers the 256 CUs
+    // 128 x 192 tiles once they make three quarters of a round of
+    // workgroups (two per CU) or more, else 64 x 64 tiles (measured:
+    // 1024 x 12288 x 3072 123.5 -> 94.8 us with 512 large tiles; 1536 x 3072
+    // x 3072 with 192 large tiles 74.7 us against 54.5 for small ones).
+    if (!(n_out % 192 == 0 && static_cast<long long>((m + 127) / 128) * (n_out / 192) >= 384) &&
+        (m <= 1024 || n_out % 192 == 0))
+        return 3;
+    // 256 x 256 tiles (eight waves, one workgroup per CU: each weight is
+    // dequantised for twice the rows) when they still give three or more
+    // workgroups per CU; measured 11 % faster at 4096 x 12288 x 3072.
+    if (n_out % 256 == 0 && static_cast<long long>((m + 255) / 256) * (n_out / 256) >= 768) return 5;
+    if (n_out % 192 == 0) return 4;
+    return 6;
+}
+
 // Kernel shape for m rows and n_out outputs per stream (measured on
 // MI355X), and its launch.  m_split = 0: one stream (n = n_out).  m_split >
 // 0: the two streams' diagonal blocks over the stacked rows (n = 2 n_out
@@ -625,40 +649,7 @@ static int dispatch_w4a16(const void *x, const void *codes, const void *scales, 
                           int out_type, int epi, int m, int n, int k, int n_part, OutMap out, int m_split,
                           hipStream_t s) {
     const int n_out = out.n_out;
-    // QI_HIP_W4A16_TILES forces a shape, for tuning: 1 K-split 64 x 64, 2
-    // tiled 32 x 64, 3 tiled 64 x 64, 4 tiled 128 x 192, 5 tiled 256 x 256, 6 tiled
-    // 128 x 128.
-    static const int forced = [] {
-        const char *e = getenv("QI_HIP_W4A16_TILES");
-        return e ? atoi(e) : -1;
-    }();
-    int cfg;  // 1 K-split, 2..4 as above, 5 tiled 256 x 256, 6 tiled 128 x 128
-    if (forced >= 1 && forced <= 6 && (forced != 4 || n_out % 192 == 0) && (forced != 5 || n_out % 256 == 0))
-        cfg = forced;
-    // Short M with few column tiles (the text stream's 256 x 3072 outputs):
-    // the tiled grid is too small to fill the chip, so split K across the
-    // workgroup's waves instead (measured: 256 x 3072 x 3072 20.4 -> 17.5 us,
-    // 256 x 3072 x 12288 67.4 -> 49.3 us; wider N keeps the tiled kernel).
-    else if (m <= 256 && static_cast<long long>((m + 31) / 32) * ((n_out + 63) / 64) < 1024)
-        cfg = 1;
-    else if (m <= 256)
-        cfg = 2;  // short row tiles so the grid still covers the 256 CUs
-    // 128 x 192 tiles once they make three quarters of a round of
-    // workgroups (two per CU) or more, else 64 x 64 tiles (measured:
-    // 1024 x 12288 x 3072 123.5 -> 98.4 us with 512 large tiles; 1536 x 3072
-    // x 3072 with 192 large tiles 74.7 us against 63.9 for small ones).
-    else if (!(n_out % 192 == 0 && static_cast<long long>((m + 127) / 128) * (n_out / 192) >= 384) &&
-             (m <= 1024 || n_out % 192 == 0))
-        cfg = 3;
-    // 256 x 256 tiles (eight waves, one workgroup per CU: each weight is
-    // dequantised for twice the rows) when they still give three or more
-    // workgroups per CU; measured 11 % faster at 4096 x 12288 x 3072.
-    else if (n_out % 256 == 0 && static_cast<long long>((m + 255) / 256) * (n_out / 256) >= 768)
-        cfg = 5;
-    else if (n_out % 192 == 0)
-        cfg = 4;
-    else
-        cfg = 6;
+    const int cfg = select_w4a16_tiles(m, n_out);
     const int bm[] = {0, 64, 32, 64, 128, 256, 128}, bn[] = {0, 64, 64, 64, 192, 256, 128};
     // One launch over both streams only when its tiles fit both blocks and
     // it takes no more rounds of workgroups than stream 0 alone (these
@@ -747,4 +738,9 @@ QI_API int qi_hip_w4a16_gemm_tiled(const void *x_half, const void *w_tiled_codes
                                    void *stream) {
     return qi_hip_w4a16_gemm_tiled_parts(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
                                          n, stream);
+}
+
+QI_API int qi_hip_w4a16_tiles(int m, int n_out) {
+    if (m <= 0 || n_out <= 0) return -1;
+    return m <= 16 ? 0 : select_w4a16_tiles(m, n_out);
 }

@@ -33,7 +33,6 @@
 // The matrix-core work of group g + 1 is interleaved, tile by tile, with the
 // fp32 step of group g, so the two units work side by side within a wave.
 
-#include <cstdlib>
 #include <utility>
 
 #include "qi_common.h"
@@ -534,33 +533,26 @@ using namespace qi;
 
 namespace qi {
 
+// Tile shapes for one stream of m rows and n outputs (measured on
+// MI355X): 0 = 128 x 128 tiles with four waves when that already gives two
+// workgroups per CU (persistent when m and n are multiples of 128);
+// otherwise, for short M, 3 = 64 x 128 four-wave tiles when N is wide, or
+// 4 = single-wave 32 x 32 tiles with an 8-deep ring.
+static int select_fp6_tiles(int m, int n) {
+    if (static_cast<long long>((m + 127) / 128) * ((n + 127) / 128) >= 512) return 0;
+    return n >= 8192 ? 3 : 4;
+}
+
 // Tile-shape choice for one stream (see qi_hip_w4a4_gemm_fp6_parts); the
 // arguments are checked by the callers.
 static int dispatch_fp6(const void *a_codes6, const void *w_codes6, const float *bias, void *y, int out_type,
                         int epilogue, int m, int n, int k, int n_part, Fp6Out out, hipStream_t s) {
-    // Tile shapes (measured on MI355X): 128 x 128 with four waves when that
-    // already gives two workgroups per CU (persistent when M and N are
-    // multiples of 128); otherwise, for short M, single-
-    // wave 32 x 32 tiles with an 8-deep ring, or 64 x 128 four-wave tiles
-    // when N is wide.  QI_HIP_FP6_TILES (0, 3, 4, or 5 for one 128 x 128
-    // tile per workgroup) overrides the choice, for tuning.
-    static const int forced = [] {
-        const char *e = getenv("QI_HIP_FP6_TILES");
-        return e ? atoi(e) : -1;
-    }();
-    int cfg;
-    if (static_cast<long long>((m + 127) / 128) * ((n + 127) / 128) >= 512)
-        cfg = 0;
-    else
-        cfg = n >= 8192 ? 3 : 4;
-    if (forced >= 0) cfg = forced;
+    const int cfg = select_fp6_tiles(m, n);
     switch (cfg) {
     case 0:
         // The persistent kernel takes whole 128 x 128 tiles only.
         if (m % 128 == 0 && n % 128 == 0)
             return launch_fp6_persistent(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, out, 0, s);
-        return launch_fp6<2, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, out, s);
-    case 5:
         return launch_fp6<2, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, out, s);
     case 3:
         return launch_fp6<1, 2, 2, 2, 4>(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n_part, out, s);
@@ -608,12 +600,8 @@ QI_API int qi_hip_w4a4_gemm_fp6_dual(const void *a_codes6, const void *w_codes6,
         static_cast<long long>(2 * (n / 32)) * g * FP6_BLOCK >= (1LL << 31))
         return kInvalid;
     hipStream_t s = stream_of(stream);
-    static const int forced = [] {
-        const char *e = getenv("QI_HIP_FP6_TILES");
-        return e ? atoi(e) : -1;
-    }();
     // Both streams in one persistent launch when every tile is whole.
-    if ((forced < 0 || forced == 0) && m % 128 == 0 && m_split % 128 == 0 && n % 128 == 0)
+    if (m % 128 == 0 && m_split % 128 == 0 && n % 128 == 0)
         return launch_fp6_persistent(a_codes6, w_codes6, bias, y, out_type, epilogue, m, 2 * n, k, n_part,
                                      Fp6Out{0, m, n}, m_split, s);
     // Otherwise one launch per stream, each writing its rows of y.
@@ -629,4 +617,11 @@ QI_API int qi_hip_w4a4_gemm_fp6_dual(const void *a_codes6, const void *w_codes6,
 QI_API int qi_hip_w4a4_gemm_fp6(const void *a_codes6, const void *w_codes6, const float *bias, void *y,
                                 int out_type, int epilogue, int m, int n, int k, void *stream) {
     return qi_hip_w4a4_gemm_fp6_parts(a_codes6, w_codes6, bias, y, out_type, epilogue, m, n, k, n, stream);
+}
+
+QI_API int qi_hip_w4a4_fp6_tiles(int m, int n) {
+    if (m <= 0 || n <= 0) return -1;
+    const int cfg = select_fp6_tiles(m, n);
+    // 1: the persistent form of the 128 x 128 tiles.
+    return cfg == 0 && m % 128 == 0 && n % 128 == 0 ? 1 : cfg;
 }

@@ -40,6 +40,8 @@ SIGNATURES: dict[str, list] = {
     "qi_hip_w4a4_gemm_fp6_dual": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p],
     "qi_hip_w4a16_gemm_tiled_parts": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p],
     "qi_hip_w4a16_gemm_tiled_dual": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p],
+    "qi_hip_w4a16_tiles": [_i, _i],
+    "qi_hip_w4a4_fp6_tiles": [_i, _i],
     "qi_flash_attention": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
     "qi_hip_flash_attention": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p],
     "qi_hip_layer_norm_scale": [_p, _p, _i, _p, _i, _i, _i, _i, _p],
@@ -57,7 +59,7 @@ SIGNATURES: dict[str, list] = {
 # Entry points whose return type is not int.
 RESTYPES = {"qi_fnv1a": (_u64, [_u64, _p, _u64]), "qi_pack_close": (None, [_p])}
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib = None
 

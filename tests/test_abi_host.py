@@ -102,3 +102,32 @@ def test_missing_library_fails_loudly(tmp_path, monkeypatch):
 def test_error_wording_mirrors_reference():
     e = _lib.QiHipError("w4a4 gemm", 1)
     assert "w4a4 gemm failed" in str(e) and e.status == 1
+
+
+# The tile choices the parity tests rely on (a query: no device work).  The
+# MMDiT block's shapes: image rows 4096 (12288 for an edit with two reference
+# images), text rows 256 (512), q/k/v/out 3072, MLP 12288, fused QKV 9216.
+@pytest.mark.parametrize("m,n_out,cfg", [
+    (1, 18432, 0), (16, 18432, 0),                 # GEMV
+    (256, 3072, 1), (256, 4096, 1),                # K-split
+    (256, 9216, 2), (256, 12288, 2), (240, 9216, 2), (200, 9216, 1),
+    (1152, 192, 3), (300, 2048, 3), (1024, 256, 3),
+    (4096, 9216, 4), (4096, 3072, 4), (1152, 18432, 4), (600, 18432, 4),
+    (4096, 12288, 5), (12288, 12288, 5),
+    (1152, 1024, 6),
+])
+def test_w4a16_tile_choice(m, n_out, cfg):
+    assert qwen_image_hip.load().qi_hip_w4a16_tiles(m, n_out) == cfg
+
+
+@pytest.mark.parametrize("m,n,cfg", [
+    (4096, 9216, 1), (4096, 3072, 1), (4096, 12288, 1), (12288, 9216, 1), (2048, 6144, 1),
+    (4100, 3072, 0), (256, 9216, 3), (256, 3072, 4), (512, 3072, 4), (100, 8192, 3),
+])
+def test_fp6_tile_choice(m, n, cfg):
+    assert qwen_image_hip.load().qi_hip_w4a4_fp6_tiles(m, n) == cfg
+
+
+def test_tile_queries_reject_empty_shapes():
+    L = qwen_image_hip.load()
+    assert L.qi_hip_w4a16_tiles(0, 64) == -1 and L.qi_hip_w4a4_fp6_tiles(64, 0) == -1

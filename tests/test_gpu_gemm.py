@@ -286,19 +286,21 @@ def test_w4a16_dequant_bit_exact_identity(dev, path):
     np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("m,n,k", [(1152, 192, 128), (4096, 12288, 64)])
+@pytest.mark.parametrize("m,n,k,tiles", [(1152, 18432, 128, 4), (4096, 12288, 64, 5)])
 @pytest.mark.parametrize("mixed", [False, True])
-def test_w4a16_dequant_bit_exact_large_tiles(dev, mixed, m, n, k):
+def test_w4a16_dequant_bit_exact_large_tiles(dev, mixed, m, n, k, tiles):
     """The large-M tile shapes (m > 1024: 128 x 192 tiles, and 256 x 256
     tiles once they give 768 workgroups): x repeats the identity, so every
     output is one dequantised weight, compared bit for bit on double-rounding
     (scale, minimum) pairs -- in every group, or mixed with ordinary groups so
     both dequantisation paths run in one launch."""
+    import qwen_image_hip as q
     import qwen_image_hip.ops as ops
+    assert q.load().qi_hip_w4a16_tiles(m, n) == tiles
     G = k // 64
-    s_adv, m_adv = _double_rounding_cases(n * G, seed=5)
-    scales = s_adv.reshape(n, G).copy()
-    mins = m_adv.reshape(n, G).copy()
+    s_adv, m_adv = _double_rounding_cases(n * G, seed=5)   # ~17k distinct pairs; repeated to fill n * G
+    scales = np.resize(s_adv, n * G).reshape(n, G).copy()
+    mins = np.resize(m_adv, n * G).reshape(n, G).copy()
     if mixed:
         g = np.random.default_rng(6)
         plain = g.random((n, G)) < 0.5
