@@ -17,6 +17,7 @@ the M=1/M=2 modulation GEMV (config 4) are reported beside it.
     python bench.py --gemv-only      # the all-blocks modulation GEMV x 10 + a
                                      # 512 MiB copy, for the GEMV's counter runs
     python bench.py --w4a16-only     # the W4A16 MLP-up GEMM x 11 + a 512 MiB copy
+    python bench.py --probe-overlap  # matrix-core / vector-unit co-execution micro-benchmark
 """
 from __future__ import annotations
 
@@ -641,12 +642,74 @@ def bench_stack(blocks=STACK_BLOCKS, steps=4):
     ops_step = blocks * 2.0 * sum(n * k for _, n, k in block_shapes()) * sum(STACK_STREAMS.values())
     ms = sum(times[1:]) / max(1, len(times) - 1)
     tops = ops_step / (ms * 1e-3) / 1e12
-    del layers, b
+    result = {"workload": f"config 5: {blocks}-block W4A4 stack, image M={STACK_STREAMS['image']} + text "
+                          f"M={STACK_STREAMS['text']}", "ms_per_step": round(ms, 3),
+              "first_step_ms": round(times[0], 3), "TOPS": round(tops, 1),
+              "frac_int8_peak": round(tops * 1e12 / PEAK_INT8_OPS, 4), "steps_timed": len(times) - 1}
+    del b
+    result["prefix_variant"] = _stack_prefix_variant(q, layers, g, steps)
+    del layers
     torch.cuda.empty_cache()
-    return {"workload": f"config 5: {blocks}-block W4A4 stack, image M={STACK_STREAMS['image']} + text "
-                        f"M={STACK_STREAMS['text']}", "ms_per_step": round(ms, 3),
-            "first_step_ms": round(times[0], 3), "TOPS": round(tops, 1),
-            "frac_int8_peak": round(tops * 1e12 / PEAK_INT8_OPS, 4), "steps_timed": len(times) - 1}
+    return result
+
+
+def _stack_prefix_variant(q, layers, g, steps):
+    """The reference's own call pattern for the same edit
+    (qwen_image_cuda/src/transformer.cplus:822-1017): the prefix rows (512
+    text + 2 x 4096 condition-image rows) run through the 60 blocks once,
+    their keys and values cached, and each denoising step then runs only the
+    4096 rows of the image being generated.  Here: the prefix as one
+    dual-stream pass (condition rows on the image stream's weights, text rows
+    on the text stream's), timed once; each step the image stream's records
+    alone at M = 4096; `steps` steps timed one by one, the first reported
+    apart.  Linears only, as the stack above."""
+    import torch
+
+    m_img = STACK_STREAMS["image"] // 3
+    m_pre = STACK_STREAMS["image"] - m_img + STACK_STREAMS["text"]
+    split = STACK_STREAMS["image"] - m_img
+    lin, f16 = q.linear, torch.float16
+
+    def buffers(m):
+        return {"x_qkv": heavy_tailed(m, HIDDEN, g), "x_out": heavy_tailed(m, HIDDEN, g),
+                "x_mlp": heavy_tailed(m, HIDDEN, g), "work": q.Work(m, MLP, "cuda"),
+                "y": torch.empty((m, HIDDEN), dtype=f16, device="cuda"),
+                "qkv": torch.empty((3, m, HIDDEN), dtype=f16, device="cuda"),
+                "h": torch.empty((m, MLP), dtype=f16, device="cuda")}
+
+    def run(recs, b, split_rows):
+        w = b["work"]
+        for blk in recs:
+            lin(blk["qkv"], w, b["x_qkv"], b["qkv"], out_dtype=f16, split_rows=split_rows)
+            lin(blk["to_out"], w, b["x_out"], b["y"], out_dtype=f16, split_rows=split_rows)
+            lin(blk["mlp_up"], w, b["x_mlp"], b["h"], out_dtype=f16, gelu=True, split_rows=split_rows)
+            lin(blk["mlp_down"], w, b["h"], b["y"], out_dtype=f16, split_rows=split_rows)
+
+    def timed(fn):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1)
+
+    bp = buffers(m_pre)
+    prefix_ms = timed(lambda: run(layers, bp, split))
+    del bp
+    image_layers = [{name: rec.stream(0) for name, rec in blk.items()} for blk in layers]
+    bi = buffers(m_img)
+    times = [timed(lambda: run(image_layers, bi, None)) for _ in range(steps)]
+    del bi
+    per_block = 2.0 * sum(n * k for _, n, k in block_shapes())
+    ms = sum(times[1:]) / max(1, len(times) - 1)
+    tops = len(layers) * per_block * m_img / (ms * 1e-3) / 1e12
+    pre_tops = len(layers) * per_block * m_pre / (prefix_ms * 1e-3) / 1e12
+    return {"workload": f"prefix {m_pre} rows ({split} condition + {STACK_STREAMS['text']} text) once, then "
+                        f"{m_img} image rows per step, {len(layers)} blocks",
+            "prefix_ms": round(prefix_ms, 3), "prefix_TOPS": round(pre_tops, 1),
+            "ms_per_step": round(ms, 3), "first_step_ms": round(times[0], 3), "TOPS": round(tops, 1),
+            "frac_int8_peak": round(tops * 1e12 / PEAK_INT8_OPS, 4),
+            "ms_for_4_steps_with_prefix": round(prefix_ms + 4 * ms, 3)}
 
 
 def cpu_baseline(budget_s=20.0):
@@ -657,12 +720,9 @@ def cpu_baseline(budget_s=20.0):
     GEMMs that ran / their time (weights packed outside the timed part)."""
     import numpy as np
 
-    sys.path.insert(0, str(ROOT / "oracle"))
-    sys.path.insert(0, str(ROOT / "tests"))
-    import oracle
+    oracle = _cpu_oracle()
     from _data import heavy_tailed as ht, weights_f16
 
-    oracle.lib()
     done_ops, spent, ran = 0.0, 0.0, []
     seed = 10
     for stream, m in STREAMS.items():
@@ -686,6 +746,120 @@ def cpu_baseline(budget_s=20.0):
             "sample": f"CPU oracle W4A4 quantise + GEMM over {len(ran)} of the block's 12 linears "
                       f"({', '.join(ran)}), {done_ops / 1e9:.1f} G int-ops in {spent:.1f} s on "
                       f"{oracle.num_threads()} threads ({platform.processor() or platform.machine()})"}
+
+
+PROBE_BODIES = {0: "fp6 MFMA x4 (4 chains)", 1: "fp32 FMA x64", 2: "MFMA x4 + FMA x64 interleaved, independent",
+                3: "W4A4 per-group mix: fp6 MFMA x4 + f32 outer MFMA x2 + FMA x64 on their results",
+                4: "FMA x32, MFMA x2, FMA x32, MFMA x2 (independent)"}
+
+
+def probe_overlap(iters=2000):
+    """Matrix-core / vector-unit co-execution on this MI355X
+    (probe/mfma_valu_probe.hip): shader clocks per loop iteration and wave
+    for each body, at one and two waves per SIMD, with MFMA results in
+    ordinary VGPRs (the product's build) and in accumulator registers."""
+    import ctypes
+
+    import torch
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    seed = torch.randint(0, 1 << 30, (64,), dtype=torch.int32, device="cuda")
+    out = {"cus": cus, "iters": iters, "unit": "shader clocks per iteration per wave (s_memtime)",
+           "bodies": PROBE_BODIES}
+    for form in ("vgpr", "agpr"):
+        lib = ctypes.CDLL(str(ROOT / "qwen-image-cplus_amd" / "probe" / f"libqi_probe_{form}.so"))
+        lib.qi_probe_run.argtypes = [ctypes.c_int] * 3 + [ctypes.c_void_p] * 4
+        for waves in (1, 2):
+            blocks = cus * waves  # four-wave workgroups: `waves` waves per SIMD
+            res = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
+            cyc = torch.empty(blocks * 4, dtype=torch.int64, device="cuda")
+            for body in PROBE_BODIES:
+                st = lib.qi_probe_run(body, blocks, iters, seed.data_ptr(), res.data_ptr(), cyc.data_ptr(),
+                                      ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+                if st:
+                    raise RuntimeError(f"probe body {body} failed ({st})")
+                ms = time_fn(lambda: lib.qi_probe_run(body, blocks, iters, seed.data_ptr(), res.data_ptr(),  # noqa
+                                                      cyc.data_ptr(), ctypes.c_void_p(
+                                                          torch.cuda.current_stream().cuda_stream)), 3, 1)
+                c = cyc.double()
+                out[f"{form}_w{waves}_body{body}"] = {
+                    "clk_per_iter_mean": round(float(c.mean()) / iters, 1),
+                    "clk_per_iter_max": round(float(c.max()) / iters, 1),
+                    "kernel_ms": round(ms, 3)}
+                log(f"probe {form} waves/SIMD={waves} body {body}: {out[f'{form}_w{waves}_body{body}']}")
+    return out
+
+
+def _cpu_oracle():
+    sys.path.insert(0, str(ROOT / "oracle"))
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle
+
+    oracle.lib()
+    return oracle
+
+
+def cpu_baseline_w4a16(budget_s=10.0):
+    """The CPU oracle's W4A16 path (dequantise to fp16 as gemm.cu:229-230,
+    then a blocked fp32 matmul, OpenMP over the host cores): config 1 (one
+    linear, M=256, N=K=3072) in full, then config 2's image-stream linears in
+    block order until about budget_s seconds have run.  TFLOP/s = 2*M*N*K of
+    the GEMMs that ran / their time (dequantisation inside the timing, weight
+    packing outside)."""
+    import numpy as np
+
+    oracle = _cpu_oracle()
+    from _data import normal_f32, weights_f16
+
+    def one(m, n, k, seed):
+        c, sc, mn = oracle.quantize_matrix(weights_f16(n, k, seed), 5)
+        xb = oracle.half_from_f32(normal_f32(m, k, seed + 1))
+        t0 = time.perf_counter()
+        oracle.gemm_f16(xb, oracle.w4a16_dequantize(c, sc, mn), precise=False)
+        return time.perf_counter() - t0
+
+    t1 = one(256, HIDDEN, HIDDEN, 1)
+    c1 = 2.0 * 256 * HIDDEN * HIDDEN
+    spent, flops, ran = 0.0, 0.0, []
+    for name, n, k in block_shapes():
+        if spent >= budget_s:
+            break
+        spent += one(STREAMS["image"], n, k, 20 + len(ran))
+        flops += 2.0 * STREAMS["image"] * n * k
+        ran.append(f"image.{name}")
+    cores = oracle.num_threads()
+    cpu = platform.processor() or platform.machine()
+    return {"value": round(flops / spent / 1e12, 6), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"CPU oracle W4A16 dequantise + blocked fp32 matmul over {len(ran)} of config 2's image-stream "
+                      f"linears ({', '.join(ran)}, M=4096), {flops / 1e9:.1f} GFLOP in {spent:.1f} s on {cores} "
+                      f"threads ({cpu})",
+            "config1_m256_n3072_k3072": {"ms": round(t1 * 1e3, 2), "TFLOP_s": round(c1 / t1 / 1e12, 6)}}
+
+
+def cpu_baseline_gemv(reps=5):
+    """The CPU oracle's W4A16 path on config 4's modulation linear
+    (3072 -> 18432) at M=1 and M=2: each weight row dequantised to fp16
+    (gemm.cu:229-230) and dotted with the input rows in fp32, OpenMP over the
+    rows; mean of `reps` calls, GB/s over the same algorithmic bytes as the
+    GPU figure."""
+    oracle = _cpu_oracle()
+    from _data import normal_f32, weights_f16
+
+    n, k = MODULATION_N, HIDDEN
+    c, sc, mn = oracle.quantize_matrix(weights_f16(n, k, 6), 5)
+    out = {"kind": "port", "cores": oracle.num_threads(), "unit": "us",
+           "sample": f"CPU oracle per-row dequantise + fp32 dots, {n}x{k} weights, mean of {reps} calls, "
+                     f"{oracle.num_threads()} threads ({platform.processor() or platform.machine()})"}
+    for m in (1, 2):
+        xb = oracle.half_from_f32(normal_f32(m, k, 7))
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            oracle.w4a16_gemv(xb, c, sc, mn)
+        t = (time.perf_counter() - t0) / reps
+        total = n * k // 2 + n * (k // 64) * 4 + m * k * 2 + m * n * 2
+        out[f"m{m}"] = {"us": round(t * 1e6, 1), "GB_s": round(total / t / 1e9, 2)}
+    out["value"] = out["m1"]["us"]
+    return out
 
 
 def bench_library(iters=50):
@@ -737,6 +911,8 @@ def main(argv=None) -> int:
     ap.add_argument("--w4a16-only", action="store_true",
                     help="run only the W4A16 MLP-up GEMM (11 launches) and a 512 MiB device copy (5 launches), "
                          "for hardware-counter runs")
+    ap.add_argument("--probe-overlap", action="store_true",
+                    help="only the matrix-core / vector-unit co-execution micro-benchmark (probe/)")
     ap.add_argument("--library-only", action="store_true",
                     help="only the calibration: the vendor library's plain fp16 / int8 GEMMs at the block's shapes")
     args = ap.parse_args(argv)
@@ -761,6 +937,9 @@ def main(argv=None) -> int:
         return 0
     if args.library_only:
         print(json.dumps({"library_gemm": bench_library()}), flush=True)
+        return 0
+    if args.probe_overlap:
+        print(json.dumps({"mfma_valu_probe": probe_overlap()}), flush=True)
         return 0
     log("packing W4A4 block weights (fp6 operands)")
     blk4 = Block(q.SCHEME_W4A4_H256, 1)
@@ -859,6 +1038,12 @@ def main(argv=None) -> int:
         log("cpu baseline")
         cpu = cpu_baseline()
         log(f"cpu: {cpu}")
+        if "w4a16_block" in extra:
+            extra["w4a16_block"]["cpu_baseline"] = cpu_baseline_w4a16()
+            log(f"cpu w4a16: {extra['w4a16_block']['cpu_baseline']}")
+        if "modulation_gemv" in extra:
+            extra["modulation_gemv"]["cpu_baseline"] = cpu_baseline_gemv()
+            log(f"cpu gemv: {extra['modulation_gemv']['cpu_baseline']}")
 
     line = {
         "metric": "QIPACK W4A4/W4A16 linear TOPS + % roofline, MMDiT block @1024^2 (M=4352)",

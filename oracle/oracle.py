@@ -53,6 +53,7 @@ def lib() -> ctypes.CDLL:
         L.qo_w4a16_dequantize.argtypes = [_P, _P, _P, _P, _I64, _I64]
         L.qo_gemm_f16.argtypes = [_P, _P, _P, _I64, _I64, _I64, _I]
         L.qo_sgemm_nt.argtypes = [_P, _P, _P, _I64, _I64, _I64]
+        L.qo_w4a16_gemv.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64]
         L.qo_gelu_tanh.argtypes = [ctypes.c_float]
         L.qo_gelu_tanh.restype = ctypes.c_float
         L.qo_fnv1a.argtypes = [ctypes.c_uint64, _P, ctypes.c_uint64]
@@ -183,6 +184,17 @@ def gemm_f16(x_bits, w_bits, precise=True) -> np.ndarray:
 
 def w4a16_gemm(x_bits, codes, scales, mins, precise=True) -> np.ndarray:
     return gemm_f16(x_bits, w4a16_dequantize(codes, scales, mins), precise)
+
+
+def w4a16_gemv(x_bits, codes, scales, mins) -> np.ndarray:
+    """W4A16 for a few rows with per-row dequantisation and fp32 dots (the
+    CPU baseline of the modulation linears)."""
+    x, c, s, mn = _c(x_bits, np.uint16), _c(codes, np.uint8), _c(scales, np.uint16), _c(mins, np.uint16)
+    m, k = x.shape
+    n = c.shape[0]
+    y = np.zeros((m, n), np.float32)
+    lib().qo_w4a16_gemv(_p(x), _p(c), _p(s), _p(mn), _p(y), m, n, k)
+    return y
 
 
 def gelu_tanh(v) -> np.ndarray:

@@ -453,6 +453,45 @@ QO_EXPORT void qo_sgemm_nt(const float *x, const float *w, float *y, int64_t m, 
         }
 }
 
+/* W4A16 for a few rows (the GEMV shapes) without materialising the
+ * dequantised matrix: per weight row, fp16(fmaf(code, scale, minimum))
+ * (gemm.cu:229-230) widened to fp32 -- formed once per group for the 16
+ * possible codes -- then an fp32 dot product with each of the m fp16 input
+ * rows.  The CPU baseline of the modulation linears (no
+ * reference counterpart: the reference has no CPU GEMM for this path). */
+QO_EXPORT void qo_w4a16_gemv(const uint16_t *x, const uint8_t *codes, const uint16_t *scales,
+                             const uint16_t *minimums, float *y, int64_t m, int64_t n, int64_t k) {
+    int64_t groups = k / 64;
+    float *xf = (float *)malloc((size_t)(m * k) * sizeof(float));
+    for (int64_t i = 0; i < m * k; ++i) xf[i] = qo_half_to_f32(x[i]);
+#pragma omp parallel
+    {
+        float *wr = (float *)malloc((size_t)k * sizeof(float));
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < n; ++r) {
+            for (int64_t g = 0; g < groups; ++g) {
+                /* The group's 16 possible weights, then a table lookup per code. */
+                float scale = qo_half_to_f32(scales[r * groups + g]);
+                float minimum = qo_half_to_f32(minimums[r * groups + g]);
+                float table[16];
+                for (int c = 0; c < 16; ++c) table[c] = qo_half_round(fmaf((float)c, scale, minimum));
+                const uint8_t *cb = codes + r * (k / 2) + g * 32;
+                for (int i = 0; i < 32; ++i) {
+                    wr[g * 64 + 2 * i] = table[cb[i] & 0x0F];
+                    wr[g * 64 + 2 * i + 1] = table[cb[i] >> 4];
+                }
+            }
+            for (int64_t a = 0; a < m; ++a) {
+                float total = 0.0f;
+                for (int64_t i = 0; i < k; ++i) total += xf[a * k + i] * wr[i];
+                y[a * n + r] = total;
+            }
+        }
+        free(wr);
+    }
+    free(xf);
+}
+
 /* ops.cu:156-160 (gelu_tanh_kernel). */
 QO_EXPORT float qo_gelu_tanh(float v) {
     return 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));

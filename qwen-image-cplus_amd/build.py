@@ -96,6 +96,24 @@ def build_cli() -> Path:
     return CLI
 
 
+PROBE = PKG / "probe"
+
+
+def build_probe() -> list[Path]:
+    """The matrix-core / vector-unit co-execution micro-benchmark
+    (probe/mfma_valu_probe.hip, run by ``bench.py --probe-overlap``), built
+    with MFMA results in ordinary VGPRs (the product library's flag) and in
+    accumulator registers (the compiler's default).  Not part of the
+    product library."""
+    out = []
+    agpr = [f for f in HIP_FLAGS if f not in ("-mllvm", "-amdgpu-mfma-vgpr-form=1")]
+    for form, flags in (("vgpr", HIP_FLAGS), ("agpr", agpr)):
+        lib = PROBE / f"libqi_probe_{form}.so"
+        _run([HIPCC, *flags, "-shared", "-o", str(lib), str(PROBE / "mfma_valu_probe.hip")])
+        out.append(lib)
+    return out
+
+
 def build_oracle() -> Path:
     subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], check=True)
     return ROOT / "oracle" / "_build" / "libqi_oracle.so"
@@ -109,6 +127,7 @@ def main(argv=None) -> int:
     print("built", build_library(args.j))
     print("built", build_cli())
     if not args.lib_only:
+        print("built", *build_probe())
         print("built", build_oracle())
     return 0
 

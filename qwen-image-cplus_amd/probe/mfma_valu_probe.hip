@@ -1,0 +1,156 @@
+// Micro-benchmark of matrix-core / vector-unit co-execution on gfx950, the
+// measurement behind the W4A4 kernel's instruction mix (not part of the
+// product library; built twice by build.py: MFMA results in ordinary VGPRs,
+// as the product is compiled, and in accumulator registers, the compiler's
+// default).
+//
+// Each wave runs `iters` iterations of one of these bodies on values held in
+// registers (no memory traffic inside the timed loop):
+//   0  four independent fp6 32x32x64 MFMAs (v_mfma_scale_f32_32x32x64_f8f6f4),
+//      each accumulating into its own tile (four dependence chains)
+//   1  64 independent fp32 FMAs (v_fmac_f32, 64 accumulators)
+//   2  bodies 0 and 1 interleaved (one MFMA, then 16 FMAs), no dependences
+//   3  the W4A4 kernel's per-group mix for a 64 x 64 wave tile: four fp6
+//      MFMAs (the integer partials P), two f32 32x32x1 outer-product MFMAs
+//      (sa * sw), and 64 FMAs y = fma(P, sa * sw, y) that consume the
+//      previous iteration's MFMA results, each partial tile re-issued right
+//      after its FMAs (the kernel's software pipeline)
+//   4  body 0 with the MFMAs issued in pairs after every 32 FMAs of body 1
+// and records s_memtime (shader clock) around the loop.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
+
+template <typename T>
+__device__ __forceinline__ void opaque(T &v) {
+    asm volatile("" : "+v"(v));
+}
+
+
+// One fp6 MFMA with C = 0 (the kernel's form).
+__device__ __forceinline__ v16f mfma6(v8i a, v8i b) {
+    v16f z = {};
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, z, 2, 2, 0, 127, 0, 127);
+}
+// The same, accumulating into c (bodies whose results are otherwise dead).
+__device__ __forceinline__ v16f mfma6_acc(v8i a, v8i b, v16f c) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 2, 2, 0, 127, 0, 127);
+}
+
+template <int BODY>
+__global__ __launch_bounds__(256) void probe_kernel(int iters, const int *__restrict__ seed, float *__restrict__ out,
+                                                    unsigned long long *__restrict__ cycles) {
+    const int lane = threadIdx.x & 63;
+    // Four distinct A operands, made opaque (in place) every iteration, so
+    // no MFMA is merged with another or hoisted out of the loop.
+    v8i a[4], b;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) a[t][i] = seed[(lane + i + 8 * t) & 63];
+        b[i] = seed[(lane + 3 * i + 1) & 63];
+    }
+    float acc[64], x[16];
+#pragma unroll
+    for (int r = 0; r < 64; ++r) acc[r] = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x[r] = static_cast<float>(seed[(lane + r) & 63] & 7) * 0.25f;
+    const float y = 1.0009765625f;
+    v16f p[4];
+    v32f sp[2];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) p[t] = mfma6(a[t], b);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        v32f z = {};
+        sp[t] = __builtin_amdgcn_mfma_f32_32x32x1f32(x[t], x[t + 2], z, 0, 0, 0);
+    }
+    __syncthreads();
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) opaque(a[t]);
+        opaque(b);
+        if constexpr (BODY == 0) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) p[t] = mfma6_acc(a[t], b, p[t]);
+        } else if constexpr (BODY == 1) {
+#pragma unroll
+            for (int r = 0; r < 64; ++r) acc[r] = __builtin_fmaf(x[r & 15], y, acc[r]);
+        } else if constexpr (BODY == 2) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                p[t] = mfma6_acc(a[t], b, p[t]);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[16 * t + r] = __builtin_fmaf(x[r], y, acc[16 * t + r]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else if constexpr (BODY == 3) {
+            // tile t = (i, j), i = t / 2 (row tile, scale product sp[i]),
+            // j = t % 2 (n-tile, half j of sp[i]).
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int i = t / 2, j = t % 2;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[16 * t + r] = __builtin_fmaf(p[t][r], sp[i][16 * j + r], acc[16 * t + r]);
+                __builtin_amdgcn_sched_barrier(0);
+                if (j == 1) {
+                    v32f z = {};
+                    float sa = x[i], sw = x[i + 2];
+                    opaque(sa);
+                    sp[i] = __builtin_amdgcn_mfma_f32_32x32x1f32(sa, sw, z, 0, 0, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                p[t] = mfma6(a[t], b);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int r = 0; r < 32; ++r) acc[32 * h + r] = __builtin_fmaf(x[r & 15], y, acc[32 * h + r]);
+                __builtin_amdgcn_sched_barrier(0);
+                p[2 * h] = mfma6_acc(a[2 * h], b, p[2 * h]);
+                p[2 * h + 1] = mfma6_acc(a[2 * h + 1], b, p[2 * h + 1]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+    float s = 0.f;
+#pragma unroll
+    for (int r = 0; r < 64; ++r) s += acc[r];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s += p[t][r];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 32; ++r) s += sp[t][r];
+    const int gid = blockIdx.x * blockDim.x + threadIdx.x;
+    out[gid] = s;
+    if (lane == 0) cycles[gid >> 6] = t1 - t0;
+}
+
+// Runs body `body` on `blocks` workgroups of four waves; cycles[w] receives
+// wave w's loop time in shader clocks.  Returns a hipError_t.
+extern "C" __attribute__((visibility("default"))) int qi_probe_run(int body, int blocks, int iters, const int *seed,
+                                                                    float *out, unsigned long long *cycles,
+                                                                    void *stream) {
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    dim3 g(blocks), t(256);
+    switch (body) {
+    case 0: probe_kernel<0><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
+    case 1: probe_kernel<1><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
+    case 2: probe_kernel<2><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
+    case 3: probe_kernel<3><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
+    case 4: probe_kernel<4><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
+    default: return static_cast<int>(hipErrorInvalidValue);
+    }
+    return static_cast<int>(hipGetLastError());
+}

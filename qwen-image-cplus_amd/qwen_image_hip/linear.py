@@ -74,6 +74,15 @@ class PackedLinear:
         return cls(a.scheme, a.n, a.k, torch.cat([a.tiled_codes, b.tiled_codes], 0), ts, bias, a.operand,
                    a.parts, 2)
 
+    def stream(self, index: int) -> "PackedLinear":
+        """Stream `index` (0 or 1) of a dual-stream record, as a view of its
+        arrays (no copy)."""
+        if self.streams != 2 or index not in (0, 1):
+            raise ValueError("stream() takes stream 0 or 1 of a dual-stream record")
+        half = lambda t: None if t is None else t[index * (t.shape[0] // 2):(index + 1) * (t.shape[0] // 2)]  # noqa
+        return PackedLinear(self.scheme, self.n, self.k, half(self.tiled_codes), half(self.tiled_scales),
+                            half(self.bias), self.operand, self.parts, 1)
+
     @classmethod
     def fuse(cls, records: "list[PackedLinear]") -> "PackedLinear":
         """One record for several records that read the same input (the

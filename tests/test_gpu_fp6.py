@@ -291,3 +291,6 @@ def test_dual_stream_record_matches_per_stream_calls(dev, m_img, m_txt, fuse):
     else:
         torch.testing.assert_close(got[:m_img], want0, rtol=0, atol=0)
         torch.testing.assert_close(got[m_img:], want1, rtol=0, atol=0)
+    # Each stream of the pair, taken back out as a view, is the stream's record.
+    again = q.linear(pair.stream(1), w1, x[m_img:].contiguous(), out_dtype=torch.float16, gelu=True)
+    torch.testing.assert_close(again, want1, rtol=0, atol=0)

@@ -336,6 +336,19 @@ def test_gemm_f16_precise_and_blocked():
     np.testing.assert_allclose(oracle.gemm_f16(x, w, precise=False), want, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("m", [1, 2, 5])
+def test_w4a16_gemv_baseline_matches_dequantised_matmul(m):
+    """The CPU baseline of the modulation linears (per-group 16-entry weight
+    tables, fp32 dots) against the closed-form dequantised weights
+    (pinned above) times x in float64."""
+    x = f16_bits(normal_f32(m, 640, 18))
+    w = weights_f16(48, 640, 19)
+    c, s, mn = oracle.quantize_matrix(w, 5)
+    wd = oracle.w4a16_dequantize(c, s, mn).view(np.float16).astype(np.float64)
+    want = x.view(np.float16).astype(np.float64) @ wd.T
+    np.testing.assert_allclose(oracle.w4a16_gemv(x, c, s, mn), want, rtol=1e-5, atol=1e-5)
+
+
 def test_gelu_tanh_formula():
     v = np.linspace(-6, 6, 101).astype(np.float32)
     want = 0.5 * v.astype(np.float64) * (1 + np.tanh(np.sqrt(2 / np.pi) * (v + 0.044715 * v.astype(np.float64) ** 3)))
