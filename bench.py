@@ -750,7 +750,11 @@ def cpu_baseline(budget_s=20.0):
 
 PROBE_BODIES = {0: "fp6 MFMA x4 (4 chains)", 1: "fp32 FMA x64", 2: "MFMA x4 + FMA x64 interleaved, independent",
                 3: "W4A4 per-group mix: fp6 MFMA x4 + f32 outer MFMA x2 + FMA x64 on their results",
-                4: "FMA x32, MFMA x2, FMA x32, MFMA x2 (independent)"}
+                4: "FMA x32, MFMA x2, FMA x32, MFMA x2 (independent)",
+                5: "body 3 in the product kernel's order (partial tiles two tiles behind their FMAs)",
+                6: "ds_read_b128 x8 (1 KiB per wave each): LDS read throughput",
+                7: "fp32 FMA x64 on 16 accumulators (few registers)",
+                8: "direct-to-LDS loads 4 x 1 KiB per wave (L2-resident): L2 -> LDS throughput"}
 
 
 def probe_overlap(iters=2000):
@@ -769,7 +773,7 @@ def probe_overlap(iters=2000):
     for form in ("vgpr", "agpr"):
         lib = ctypes.CDLL(str(ROOT / "qwen-image-cplus_amd" / "probe" / f"libqi_probe_{form}.so"))
         lib.qi_probe_run.argtypes = [ctypes.c_int] * 3 + [ctypes.c_void_p] * 4
-        for waves in (1, 2):
+        for waves in (1, 2, 4, 8):
             blocks = cus * waves  # four-wave workgroups: `waves` waves per SIMD
             res = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
             cyc = torch.empty(blocks * 4, dtype=torch.int64, device="cuda")

@@ -16,11 +16,24 @@
 //      previous iteration's MFMA results, each partial tile re-issued right
 //      after its FMAs (the kernel's software pipeline)
 //   4  body 0 with the MFMAs issued in pairs after every 32 FMAs of body 1
+//   5  body 3 in the product kernel's order (partial tiles issued two tiles
+//      after the FMAs that free them)
+//   6  eight ds_read_b128 (1 KiB per wave each) per iteration: LDS read
+//      throughput
+//   7  64 FMAs on 16 accumulators (few registers), for issue rate against
+//      waves per SIMD
+//   8  direct-to-LDS loads, 4 KiB per wave per iteration from an
+//      L2-resident window: L2 -> LDS throughput
 // and records s_memtime (shader clock) around the loop.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// The direct-to-LDS load below sets M0 inside inline asm; nothing else here
+// uses it.
+#pragma clang diagnostic ignored "-Winline-asm"
+
 typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
 
@@ -59,15 +72,29 @@ __global__ __launch_bounds__(256) void probe_kernel(int iters, const int *__rest
 #pragma unroll
     for (int r = 0; r < 16; ++r) x[r] = static_cast<float>(seed[(lane + r) & 63] & 7) * 0.25f;
     const float y = 1.0009765625f;
-    v16f p[4];
-    v32f sp[2];
+    constexpr bool MATRIX = BODY <= 5;  // bodies that use the matrix core
+    v16f p[4] = {};
+    v32f sp[2] = {};
+    if constexpr (MATRIX) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) p[t] = mfma6(a[t], b);
+        for (int t = 0; t < 4; ++t) p[t] = mfma6(a[t], b);
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        v32f z = {};
-        sp[t] = __builtin_amdgcn_mfma_f32_32x32x1f32(x[t], x[t + 2], z, 0, 0, 0);
+        for (int t = 0; t < 2; ++t) {
+            v32f z = {};
+            sp[t] = __builtin_amdgcn_mfma_f32_32x32x1f32(x[t], x[t + 2], z, 0, 0, 0);
+        }
     }
+    __shared__ __attribute__((aligned(16))) v4i lds[8][256];
+    if constexpr (BODY == 6) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) lds[r][threadIdx.x] = v4i{r, lane, 1, 2};
+    }
+    typedef int v4i_rsrc __attribute__((ext_vector_type(4)));
+    const uint64_t base = reinterpret_cast<uint64_t>(out);
+    const v4i_rsrc rsrc = {static_cast<int>(base), static_cast<int>((base >> 32) & 0xFFFF), 256 * 1024, 0x00020000};
+    v4i rd[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) rd[r] = v4i{0, 0, 0, 0};
     __syncthreads();
     const unsigned long long t0 = __builtin_amdgcn_s_memtime();
     for (int it = 0; it < iters; ++it) {
@@ -108,7 +135,65 @@ __global__ __launch_bounds__(256) void probe_kernel(int iters, const int *__rest
                 p[t] = mfma6(a[t], b);
                 __builtin_amdgcn_sched_barrier(0);
             }
-        } else {
+        } else if constexpr (BODY == 5) {
+            // Body 3 in the order of the product kernel's group step: the
+            // FMAs of tile q, the scale product of row tile i after its last
+            // n-tile, and the partial tile of tile q - 2 (two tiles of
+            // look-ahead for its operands).
+#pragma unroll
+            for (int q = 0; q < 6; ++q) {
+                if (q < 4) {
+                    const int i = q / 2, j = q % 2;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        acc[16 * q + r] = __builtin_fmaf(p[q][r], sp[i][16 * j + r], acc[16 * q + r]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (j == 1) {
+                        v32f z = {};
+                        float sa = x[i], sw = x[i + 2];
+                        opaque(sa);
+                        sp[i] = __builtin_amdgcn_mfma_f32_32x32x1f32(sa, sw, z, 0, 0, 0);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+                if (q >= 2) {
+                    p[q - 2] = mfma6(a[q - 2], b);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        } else if constexpr (BODY == 7) {
+            // Body 1 on 16 accumulators (few registers: up to eight waves
+            // per SIMD fit): vector-unit issue rate against waves per SIMD.
+#pragma unroll
+            for (int rep = 0; rep < 4; ++rep)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[r] = __builtin_fmaf(x[r], y, acc[r]);
+        } else if constexpr (BODY == 8) {
+            // Direct-to-LDS loads (buffer_load_dwordx4 ... lds), four 1 KiB
+            // wave loads per iteration from an L2-resident 256 KiB window of
+            // `out`, at most eight in flight: L2 -> LDS throughput.
+            const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t off = __builtin_amdgcn_readfirstlane(
+                    static_cast<uint32_t>(((blockIdx.x * 4 + wv) * 4 + t + 16 * it) & 255) * 1024u);
+                const uint32_t dst = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+                    (const __attribute__((address_space(3))) uint8_t *)&lds[2 * wv + (t & 1)][0])));
+                asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(dst),
+                             "v"(static_cast<uint32_t>(lane * 16)), "s"(rsrc), "s"(off)
+                             : "memory", "m0");
+            }
+            asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        } else if constexpr (BODY == 6) {
+            // LDS read throughput: eight ds_read_b128 per iteration (1 KiB
+            // each per wave), consumed by one integer add each.
+            const int wv = threadIdx.x >> 6;
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                v4i v = lds[(r + it) & 7][64 * wv + lane];
+                rd[r] += v;
+            }
+        } else if constexpr (BODY == 4) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
 #pragma unroll
@@ -120,18 +205,24 @@ __global__ __launch_bounds__(256) void probe_kernel(int iters, const int *__rest
             }
         }
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+    __syncthreads();
     float s = 0.f;
 #pragma unroll
     for (int r = 0; r < 64; ++r) s += acc[r];
+    if constexpr (MATRIX) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s += p[t][r];
+            for (int r = 0; r < 16; ++r) s += p[t][r];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int r = 0; r < 32; ++r) s += sp[t][r];
+            for (int r = 0; r < 32; ++r) s += sp[t][r];
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r) s += static_cast<float>(rd[r][0] + rd[r][1] + rd[r][2] + rd[r][3]);
     const int gid = blockIdx.x * blockDim.x + threadIdx.x;
     out[gid] = s;
     if (lane == 0) cycles[gid >> 6] = t1 - t0;
@@ -150,6 +241,13 @@ extern "C" __attribute__((visibility("default"))) int qi_probe_run(int body, int
     case 2: probe_kernel<2><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
     case 3: probe_kernel<3><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
     case 4: probe_kernel<4><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
+    case 5: probe_kernel<5><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
+    case 6: probe_kernel<6><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
+    case 7: probe_kernel<7><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
+    case 8:
+        if (blocks * 256 < 64 * 1024) return static_cast<int>(hipErrorInvalidValue);  // the 256 KiB window
+        probe_kernel<8><<<g, t, 0, s>>>(iters, seed, out, cycles);
+        break;
     default: return static_cast<int>(hipErrorInvalidValue);
     }
     return static_cast<int>(hipGetLastError());
