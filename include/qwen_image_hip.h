@@ -245,6 +245,20 @@ int qi_hip_layer_norm_scale(const float *x, const float *scale, int scale_stride
                             int width, int split, void *stream);
 int qi_hip_layer_norm_scale_quantize_fp6(const float *x, const float *scale, int scale_stride, int split,
                                          void *row_stats, void *codes6, int m, int k, void *stream);
+/* qi_hip_layer_norm_scale_quantize_fp6 without a caller workspace, for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid allocation).  No counterpart in
+ * the reference.  Same arguments, kernels and codes as
+ * qi_hip_layer_norm_scale_quantize_fp6 minus row_stats: the row statistics
+ * live in a fixed device array of QI_HIP_NOALLOC_MAX_ROWS rows (8 bytes per
+ * row) that the library holds on each GPU it runs on until the process
+ * ends.  It calls no allocator.  m > QI_HIP_NOALLOC_MAX_ROWS returns
+ * hipErrorInvalidValue before any launch.  All calls on one GPU share that
+ * array: calls that overlap on one GPU (concurrent streams or threads) race
+ * and must be serialised by the caller. */
+#define QI_HIP_NOALLOC_MAX_ROWS 65536
+int qi_hip_layer_norm_scale_quantize_fp6_noalloc(const float *x, const float *scale, int scale_stride, int split,
+                                                 void *codes6, int m, int k, void *stream);
 int qi_hip_swiglu(const float *gate, const float *up, void *out, int out_type, unsigned long long count,
                   void *stream);
 int qi_hip_swiglu_quantize_fp6(const float *gate, const float *up, void *codes6, int m, int k, void *stream);

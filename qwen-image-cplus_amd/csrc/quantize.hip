@@ -14,6 +14,7 @@
 // shuffles.  A row of any length is just more chunks, so there is no per-row
 // LDS limit, and the grid has m * k / 256 wavefronts to spread over the CUs.
 
+#include <mutex>
 #include <type_traits>
 
 #include "qi_common.h"
@@ -550,6 +551,67 @@ QI_API int qi_hip_layer_norm_scale_quantize_fp6(const float *x, const float *sca
     if (st) return st;
     return launch_fp6_strip<float>(x, codes6, nullptr, m, k, s,
                                    LnScaleProducer{static_cast<const float2 *>(row_stats), scale, scale_stride, split});
+}
+
+// ---------------------------------------------------------------------------
+// The same fused LayerNorm -> quantise without a caller workspace and
+// without allocating: the row statistics go to `scratch`, a fixed device
+// array that each GPU the library runs on holds until the process ends.
+// Every call on a GPU uses that GPU's array (calls that overlap on one GPU
+// race); ln_stats_kernel writes every row it covers before the quantiser
+// reads it, so nothing needs clearing between calls.
+namespace {
+
+static __device__ __align__(256) float2 scratch[QI_HIP_NOALLOC_MAX_ROWS];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+float2 *scratch_address[kMaxDevices] = {};
+
+// The current device's copy of `scratch` (its device address, looked up once
+// per device with that device current); null with *status set on failure.
+float2 *scratch_for_current_device(int *status) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        *status = static_cast<int>(e);
+        return nullptr;
+    }
+    if (dev < 0 || dev >= kMaxDevices) {
+        *status = static_cast<int>(hipErrorInvalidDevice);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    if (!scratch_address[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            *status = static_cast<int>(e != hipSuccess ? e : hipErrorInvalidSymbol);
+            return nullptr;
+        }
+        scratch_address[dev] = static_cast<float2 *>(p);
+    }
+    return scratch_address[dev];
+}
+
+}  // namespace
+
+QI_API int qi_hip_layer_norm_scale_quantize_fp6_noalloc(const float *x, const float *scale, int scale_stride,
+                                                        int split, void *codes6, int m, int k, void *stream) {
+    using namespace qi;
+    if (m > QI_HIP_NOALLOC_MAX_ROWS) return kInvalid;
+    if (m < 0 || k <= 0 || k % 256 || scale_stride < 0) return kInvalid;
+    if (m == 0) return 0;
+    if (!x || !scale || !codes6 || !aligned16(x) || !aligned16(scale) || scale_stride % 4 || !aligned16(codes6))
+        return kInvalid;
+    int status = 0;
+    float2 *stats = scratch_for_current_device(&status);
+    if (!stats) return status;
+    hipStream_t s = stream_of(stream);
+    ln_stats_kernel<<<dim3(static_cast<unsigned>((m + 3) / 4)), dim3(4 * WAVE), 0, s>>>(x, stats, m, k);
+    const int st = launch_status();
+    if (st) return st;
+    return launch_fp6_strip<float>(x, codes6, nullptr, m, k, s, LnScaleProducer{stats, scale, scale_stride, split});
 }
 
 QI_API int qi_hip_swiglu(const float *gate, const float *up, void *out, int out_type, unsigned long long count,

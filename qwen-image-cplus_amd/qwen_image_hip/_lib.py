@@ -46,6 +46,7 @@ SIGNATURES: dict[str, list] = {
     "qi_hip_flash_attention": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p],
     "qi_hip_layer_norm_scale": [_p, _p, _i, _p, _i, _i, _i, _i, _p],
     "qi_hip_layer_norm_scale_quantize_fp6": [_p, _p, _i, _i, _p, _p, _i, _i, _p],
+    "qi_hip_layer_norm_scale_quantize_fp6_noalloc": [_p, _p, _i, _i, _p, _i, _i, _p],
     "qi_hip_swiglu": [_p, _p, _p, _i, _u64, _p],
     "qi_hip_swiglu_quantize_fp6": [_p, _p, _p, _i, _i, _p],
     # QIPACK1 container (host I/O; QI_PACK_* status codes, not hipError_t).

@@ -131,3 +131,12 @@ def test_fp6_tile_choice(m, n, cfg):
 def test_tile_queries_reject_empty_shapes():
     L = qwen_image_hip.load()
     assert L.qi_hip_w4a16_tiles(0, 64) == -1 and L.qi_hip_w4a4_fp6_tiles(64, 0) == -1
+
+
+def test_noalloc_entry_point_rejects_sizes_beyond_its_array():
+    """The no-allocation LayerNorm -> quantise entry point refuses more rows
+    than its fixed statistics array holds (65536), before touching a GPU."""
+    L = qwen_image_hip.load()
+    assert L.qi_hip_layer_norm_scale_quantize_fp6_noalloc(16, 16, 256, 0, 16, 65537, 256, None) == INVALID
+    assert L.qi_hip_layer_norm_scale_quantize_fp6_noalloc(16, 16, 256, 0, 16, 4, 300, None) == INVALID  # k % 256
+    assert L.qi_hip_layer_norm_scale_quantize_fp6_noalloc(16, 16, 256, 0, 16, 0, 256, None) == 0          # no rows
