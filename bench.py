@@ -917,6 +917,8 @@ def main(argv=None) -> int:
                          "for hardware-counter runs")
     ap.add_argument("--probe-overlap", action="store_true",
                     help="only the matrix-core / vector-unit co-execution micro-benchmark (probe/)")
+    ap.add_argument("--w4a16-block-only", action="store_true",
+                    help="only the W4A16 block (config 2), printed as JSON (for kernel traces)")
     ap.add_argument("--library-only", action="store_true",
                     help="only the calibration: the vendor library's plain fp16 / int8 GEMMs at the block's shapes")
     args = ap.parse_args(argv)
@@ -941,6 +943,14 @@ def main(argv=None) -> int:
         return 0
     if args.library_only:
         print(json.dumps({"library_gemm": bench_library()}), flush=True)
+        return 0
+    if args.w4a16_block_only:
+        blk16 = Block(q.SCHEME_W4A16, 3)
+        step16 = StepW4A16(blk16, 4)
+        ms16 = time_fn(step16, args.steps, args.warmup)
+        tf16 = block_ops() / (ms16 * 1e-3) / 1e12
+        print(json.dumps({"w4a16_block": {"ms_per_step": round(ms16, 4), "TFLOP_s": round(tf16, 1),
+                                          "frac_fp16_peak": round(tf16 * 1e12 / PEAK_FP16_FLOPS, 4)}}), flush=True)
         return 0
     if args.probe_overlap:
         print(json.dumps({"mfma_valu_probe": probe_overlap()}), flush=True)
