@@ -150,9 +150,9 @@ int qi_hip_w4a16_gemm_tiled_dual(const void *x_half, const void *w_tiled_codes, 
                                  int k, int n_part, void *stream);
 
 /* The kernel shape the W4A16 GEMMs above choose for m rows and n_out
- * outputs per stream: 0 GEMV (m <= 16), 1 K-split 64 x 64 tiles, 2 tiled
- * 32 x 64, 3 tiled 64 x 64, 4 tiled 128 x 192, 5 tiled 256 x 256, 6 tiled
- * 128 x 128; -1 for m or n_out <= 0.  A query only (tests and tuning): no
+ * outputs per stream: 0 GEMV (m <= 16), 1 K-split 64 x 64 tiles, 3 tiled
+ * 64 x 64, 4 tiled 128 x 192, 5 tiled 256 x 256, 6 tiled 128 x 128; -1 for
+ * m or n_out <= 0.  A query only (tests and tuning): no
  * device work.  No counterpart in the reference, whose one W4A16 kernel has
  * a fixed tile (gemm.cu:191-268). */
 int qi_hip_w4a16_tiles(int m, int n_out);

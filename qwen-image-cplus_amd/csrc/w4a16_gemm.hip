@@ -603,15 +603,18 @@ QI_API int qi_w4a16_gemm(const void *x_half, const void *codes, const void *scal
 namespace qi {
 
 // Kernel shape for m > 16 rows and n_out outputs per stream (measured on
-// MI355X): 1 K-split 64 x 64, 2 tiled 32 x 64, 3 tiled 64 x 64, 4 tiled
-// 128 x 192, 5 tiled 256 x 256, 6 tiled 128 x 128.
+// MI355X): 1 K-split 64 x 64, 3 tiled 64 x 64, 4 tiled 128 x 192, 5 tiled
+// 256 x 256, 6 tiled 128 x 128 (2, tiled 32 x 64, is no longer chosen).
 static int select_w4a16_tiles(int m, int n_out) {
-    // Short M with few column tiles (the text stream's 256 x 3072 outputs):
+    // Short M with few 64 x 64 tiles (the text stream's 256 x 3072 outputs):
     // the tiled grid is too small to fill the chip, so split K across the
-    // workgroup's waves instead (measured: 256 x 3072 x 3072 20.4 -> 17.5 us,
-    // 256 x 3072 x 12288 67.4 -> 49.3 us; wider N keeps the tiled kernel).
-    if (m <= 256 && static_cast<long long>((m + 31) / 32) * ((n_out + 63) / 64) < 1024) return 1;
-    if (m <= 256) return 2;  // short row tiles so the grid still covers the 256 CUs
+    // workgroup's waves instead; with more tiles the 64 x 64 tiled kernel
+    // (measured on MI355X, us, K-split / 32 x 64 / 64 x 64 tiles:
+    // 256 x 3072 x 3072 16.0 / 18.7 / 19.3, 256 x 3072 x 12288 47.0 / 62.7 /
+    // 68.4, 64 x 12288 x 3072 16.9 / 20.2 / 20.3, 128 x 9216 x 3072 30.7 /
+    // 24.2 / 22.0, 256 x 9216 x 3072 47.0 / 35.8 / 30.6, 256 x 12288 x 3072
+    // 45.6 / 40.0 / 31.9).
+    if (m <= 256) return static_cast<long long>((m + 63) / 64) * ((n_out + 63) / 64) < 256 ? 1 : 3;
     // 128 x 192 tiles once they make three quarters of a round of
     // workgroups (two per CU) or more, else 64 x 64 tiles (measured:
     // 1024 x 12288 x 3072 123.5 -> 94.8 us with 512 large tiles; 1536 x 3072
@@ -665,8 +668,6 @@ static int dispatch_w4a16(const void *x, const void *codes, const void *scales, 
     switch (cfg) {
     case 1:
         return launch_splitk<4, 4>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, s);
-    case 2:
-        return launch_tiled<2, 1, 4>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, m_split, s);
     case 3:
         return launch_tiled<4, 1, 4>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, m_split, s);
     case 4:

@@ -109,8 +109,8 @@ def test_error_wording_mirrors_reference():
 # images), text rows 256 (512), q/k/v/out 3072, MLP 12288, fused QKV 9216.
 @pytest.mark.parametrize("m,n_out,cfg", [
     (1, 18432, 0), (16, 18432, 0),                 # GEMV
-    (256, 3072, 1), (256, 4096, 1),                # K-split
-    (256, 9216, 2), (256, 12288, 2), (240, 9216, 2), (200, 9216, 1),
+    (256, 3072, 1), (256, 3968, 1), (64, 12288, 1),  # K-split: under 256 64 x 64 tiles
+    (256, 4096, 3), (256, 9216, 3), (256, 12288, 3), (128, 9216, 3), (200, 9216, 3),
     (1152, 192, 3), (300, 2048, 3), (1024, 256, 3),
     (4096, 9216, 4), (4096, 3072, 4), (1152, 18432, 4), (600, 18432, 4),
     (4096, 12288, 5), (12288, 12288, 5),

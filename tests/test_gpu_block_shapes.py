@@ -68,7 +68,7 @@ def sample_rows(m, seed, splits=()):
     fixed = [0, 1, m - 2, m - 1, *edges - 1, *edges]
     for s in splits:
         fixed += [s - 2, s - 1, s, s + 1, *g.choice(np.arange(s, m), size=min(32, m - s), replace=False)]
-    rows = np.unique(np.concatenate([np.array(fixed, np.int64), g.choice(m, size=SAMPLE // 2, replace=False)]))
+    rows = np.unique(np.concatenate([np.array(fixed, np.int64), g.choice(m, size=min(SAMPLE // 2, m), replace=False)]))
     return rows[(rows >= 0) & (rows < m)]
 
 
@@ -86,8 +86,9 @@ W4A16_CASES = [
     (4096, 9216, 3072, 4),    # fused QKV: 128 x 192
     (4096, 3072, 3072, 4),    # out projection: 128 x 192
     (600, 18432, 3072, 4),    # 128 x 192 on a ragged last row band
-    (256, 12288, 3072, 2),    # text MLP up: 32 x 64 tiles
-    (240, 9216, 1024, 2),     # 32 x 64 tiles, ragged rows
+    (256, 12288, 3072, 3),    # text MLP up: 64 x 64 tiles
+    (240, 9216, 1024, 3),     # 64 x 64 tiles, ragged rows
+    (64, 12288, 3072, 1),     # K-split on a wide N
     (256, 3072, 12288, 1),    # text MLP down: K-split
     (1152, 1024, 256, 6),     # 128 x 128 tiles
     (1152, 18432, 128, 4),    # 128 x 192 tiles, two groups
