@@ -18,6 +18,7 @@ the M=1/M=2 modulation GEMV (config 4) are reported beside it.
                                      # 512 MiB copy, for the GEMV's counter runs
     python bench.py --w4a16-only     # the W4A16 MLP-up GEMM x 11 + a 512 MiB copy
     python bench.py --probe-overlap  # matrix-core / vector-unit co-execution micro-benchmark
+    python bench.py --ablate-w4a4    # the roofline kernel with parts of its work removed
 """
 from __future__ import annotations
 
@@ -866,6 +867,75 @@ def cpu_baseline_gemv(reps=5):
     return out
 
 
+ABLATION_NAMES = ("none", "dma", "lds", "barrier", "fma", "mfma", "memory", "arith_only")
+
+
+def ablate_w4a4(iters=20, reps=5):
+    """The roofline kernel's workload (dual-stream fused QKV, 4352 x 2 x 9216 x
+    3072) on the W4A4 GEMM built with parts of its work removed
+    (csrc/w4a4_fp6.hip QI_ABLATE_*, probe/libqi_fp6_ablate_*.so; outputs
+    wrong by design): median us per launch by HIP events over `reps` x
+    `iters` launches, the variants interleaved over two passes after a
+    warm-up of the unmodified build."""
+    import ctypes
+    import statistics
+
+    import torch
+    import qwen_image_hip as q
+    from qwen_image_hip import ops
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1)
+    pairs = []
+    for _ in STREAMS:
+        recs = [q.PackedLinear.from_fp16(q.SCHEME_W4A4_H256,
+                                         (torch.randn((HIDDEN, HIDDEN), generator=g, device="cuda") * 0.02).half(),
+                                         clip=True) for _ in range(3)]
+        pairs.append(q.PackedLinear.fuse(recs))
+    rec = q.PackedLinear.dual(pairs)
+    m, n, k, split = sum(STREAMS.values()), 3 * HIDDEN, HIDDEN, STREAMS["image"]
+    work = q.Work(m, k, "cuda")
+    a6 = work.fp6_views(m, k)
+    ops.quantize_activations_fp6(heavy_tailed(m, k, g), a6)
+    y = torch.empty((m, n), dtype=torch.float16, device="cuda")
+    fns = {}
+    for name in ABLATION_NAMES:
+        f = ctypes.CDLL(str(ROOT / "qwen-image-cplus_amd" / "probe" / f"libqi_fp6_ablate_{name}.so"),
+                        mode=ctypes.RTLD_LOCAL).qi_hip_w4a4_gemm_fp6_dual
+        f.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 7 + [ctypes.c_void_p]
+        fns[name] = f
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def call(name):
+        if fns[name](a6.data_ptr(), rec.tiled_codes.data_ptr(), None, y.data_ptr(), 1, 0, m, split, n, k, n, st):
+            raise RuntimeError(f"ablation build {name} failed to launch")
+
+    for _ in range(2000):
+        call("none")
+    torch.cuda.synchronize()
+    times = {name: [] for name in ABLATION_NAMES}
+    for _ in range(2):
+        for name in ABLATION_NAMES:
+            for _ in range(5):
+                call(name)
+            for _ in range(reps):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(iters):
+                    call(name)
+                e1.record()
+                e1.synchronize()
+                times[name].append(e0.elapsed_time(e1) / iters * 1e3)
+    med = {name: statistics.median(t) for name, t in times.items()}
+    return {"workload": DOMINANT_WORKLOAD, "unit": "us per launch (median)",
+            "removed": {"none": "nothing (the product kernel)", "dma": "direct-to-LDS operand loads",
+                        "lds": "fragment reads after the first group", "barrier": "per-group workgroup barrier",
+                        "fma": "exact fp32 group steps", "mfma": "matrix-core partials and scale products",
+                        "memory": "loads and fragment reads", "arith_only": "loads, fragment reads and barriers"},
+            "us": {name: round(v, 1) for name, v in med.items()},
+            "saved_us": {name: round(med["none"] - v, 1) for name, v in med.items() if name != "none"}}
+
+
 def bench_library(iters=50):
     """Calibration, not the product: the vendor library's plain GEMMs
     (torch.matmul fp16 and torch._int_mm int8 through hipBLASLt, no group
@@ -917,6 +987,8 @@ def main(argv=None) -> int:
                          "for hardware-counter runs")
     ap.add_argument("--probe-overlap", action="store_true",
                     help="only the matrix-core / vector-unit co-execution micro-benchmark (probe/)")
+    ap.add_argument("--ablate-w4a4", action="store_true",
+                    help="only the roofline kernel's ablation builds (probe/libqi_fp6_ablate_*.so), printed as JSON")
     ap.add_argument("--w4a16-block-only", action="store_true",
                     help="only the W4A16 block (config 2), printed as JSON (for kernel traces)")
     ap.add_argument("--library-only", action="store_true",
@@ -943,6 +1015,9 @@ def main(argv=None) -> int:
         return 0
     if args.library_only:
         print(json.dumps({"library_gemm": bench_library()}), flush=True)
+        return 0
+    if args.ablate_w4a4:
+        print(json.dumps({"w4a4_ablation": ablate_w4a4()}), flush=True)
         return 0
     if args.w4a16_block_only:
         blk16 = Block(q.SCHEME_W4A16, 3)

@@ -111,7 +111,22 @@ def build_probe() -> list[Path]:
         lib = PROBE / f"libqi_probe_{form}.so"
         _run([HIPCC, *flags, "-shared", "-o", str(lib), str(PROBE / "mfma_valu_probe.hip")])
         out.append(lib)
+    # The W4A4 GEMM with parts of its work removed (csrc/w4a4_fp6.hip,
+    # QI_ABLATE_*), for bench.py --ablate-w4a4: timing only, wrong outputs.
+    def ablate(item):
+        name, macros = item
+        lib = PROBE / f"libqi_fp6_ablate_{name}.so"
+        _run([HIPCC, *HIP_FLAGS, *[f"-DQI_ABLATE_{m}" for m in macros], "-shared", "-o", str(lib),
+              str(CSRC / "w4a4_fp6.hip")])
+        return lib
+    with ThreadPoolExecutor(max_workers=8) as pool:
+        out += list(pool.map(ablate, ABLATIONS.items()))
     return out
+
+
+# name -> QI_ABLATE_* macros of the W4A4 measurement builds.
+ABLATIONS = {"none": (), "dma": ("DMA",), "lds": ("LDS",), "barrier": ("BARRIER",), "fma": ("FMA",),
+             "mfma": ("MFMA",), "memory": ("DMA", "LDS"), "arith_only": ("DMA", "LDS", "BARRIER")}
 
 
 def build_oracle() -> Path:

@@ -37,6 +37,15 @@
 
 #include "qi_common.h"
 
+// Measurement builds only (build.py builds them beside the probe, bench.py
+// --ablate-w4a4 times them; their outputs are wrong by design): each
+// QI_ABLATE_* macro removes one part of the GEMM's work so that its cost
+// shows as the time saved -- QI_ABLATE_DMA the direct-to-LDS operand loads,
+// QI_ABLATE_LDS the fragment reads after the first group, QI_ABLATE_BARRIER
+// the per-group workgroup barrier, QI_ABLATE_FMA the exact fp32 group steps,
+// QI_ABLATE_MFMA the matrix-core work (partials and scale products).  The
+// product library defines none of them.
+
 namespace qi {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
@@ -150,6 +159,9 @@ __device__ __forceinline__ void fp6_tiles(uint8_t *lds, const uint8_t *__restric
     // land in the slot's unused fourth dword.
     const uint32_t lds0 = lds_address(lds);
     auto issue = [&](int g, int slot) {
+#ifdef QI_ABLATE_DMA
+        return;
+#endif
 #pragma unroll
         for (int u = 0; u < L_PER_W; ++u) {
             const int H = H0 + u;
@@ -176,12 +188,26 @@ __device__ __forceinline__ void fp6_tiles(uint8_t *lds, const uint8_t *__restric
     const uint8_t *w_frag = lds + (MT + wn * TN) * TILE + lane * 16;
     const uint8_t *x_frag = lds + wm * TM * TILE + lane * 16;
 
+#ifdef QI_ABLATE_LDS
+    bool first_read = true;
+#endif
     struct Frags {  // raw LDS reads; converted where consumed
         v8i wf[TN], xf[TM];
         uint32_t sal[TM], swl;
     };
     auto read_frags = [&](auto slot_c, Frags &F) {
         constexpr int slot = decltype(slot_c)::value;
+#ifdef QI_ABLATE_LDS
+        if (!first_read) {
+#pragma unroll
+            for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(F.wf[j]));
+#pragma unroll
+            for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(F.xf[i]), "+v"(F.sal[i]));
+            asm volatile("" : "+v"(F.swl));
+            return;
+        }
+        first_read = false;
+#endif
         uint32_t sw[TN];
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
@@ -214,6 +240,10 @@ __device__ __forceinline__ void fp6_tiles(uint8_t *lds, const uint8_t *__restric
         // Issued at raised wave priority (also the partial tiles below), so
         // the matrix core's next instruction wins issue over the other
         // wave's vector work: measured 2-3 % faster on MI355X.
+#ifdef QI_ABLATE_MFMA
+        asm volatile("" : "+v"(sp[i]));
+        return;
+#endif
         __builtin_amdgcn_s_setprio(1);
         sp[i] = __builtin_amdgcn_mfma_f32_32x32x1f32(h2f(static_cast<uint16_t>(F.swl)),
                                                      h2f(static_cast<uint16_t>(F.sal[i])), z32, 0, 0, 0);
@@ -224,12 +254,20 @@ __device__ __forceinline__ void fp6_tiles(uint8_t *lds, const uint8_t *__restric
 #pragma unroll
         for (int r = 0; r < 16; ++r) z[r] = 0.f;
         // fmt 2 = FP6 E2M3 for both operands; block scales 2^0.
+#ifdef QI_ABLATE_MFMA
+        asm volatile("" : "+v"(p[j][i]));
+        return;
+#endif
         __builtin_amdgcn_s_setprio(1);
         p[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(F.wf[j], F.xf[i], z, 2, 2, 0, 127, 0, 127);
         __builtin_amdgcn_s_setprio(0);
     };
     // The exact fp32 step of one tile and group, in ascending group order.
     auto tile_fma = [&](int j, int i) {
+#ifdef QI_ABLATE_FMA
+        asm volatile("" ::"v"(p[j][i]), "v"(sp[i]));
+        return;
+#endif
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[j][i][r] = __builtin_fmaf(p[j][i][r], sp[i][16 * j + r], acc[j][i][r]);
     };
@@ -307,7 +345,9 @@ __device__ __forceinline__ void fp6_tiles(uint8_t *lds, const uint8_t *__restric
         // groups still in flight.
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((NSTAGE - 2) * LOADS_PER_GROUP) : "memory");
+#ifndef QI_ABLATE_BARRIER
         __builtin_amdgcn_s_barrier();
+#endif
         asm volatile("" ::: "memory");
         issue(gload, u);
         if constexpr (!LAST) read_frags(std::integral_constant<int, (u + 1) % NSTAGE>{}, F);
