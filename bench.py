@@ -647,11 +647,51 @@ def bench_stack(blocks=STACK_BLOCKS, steps=4):
                           f"M={STACK_STREAMS['text']}", "ms_per_step": round(ms, 3),
               "first_step_ms": round(times[0], 3), "TOPS": round(tops, 1),
               "frac_int8_peak": round(tops * 1e12 / PEAK_INT8_OPS, 4), "steps_timed": len(times) - 1}
+    result["streamed_variant"] = _stack_streamed_variant(q, layers, b, split, denoise_step_body=lin)
     del b
     result["prefix_variant"] = _stack_prefix_variant(q, layers, g, steps)
     del layers
     torch.cuda.empty_cache()
     return result
+
+
+def _stack_streamed_variant(q, layers, b, split, denoise_step_body, steps=2):
+    """The same stack with the blocks streamed from pinned host memory
+    through two device slots (qwen_image_hip.BlockStream, the reference's
+    asynchronous block upload, transformer.cplus:503-598): per step every
+    block's 198 MB of fp6 records crosses PCIe while the previous block
+    computes.  `steps` steps timed one by one after one warm-up step."""
+    import torch
+
+    lin, f16 = denoise_step_body, torch.float16
+    t0 = time.perf_counter()
+    stream = q.BlockStream(layers)
+    pin_s = time.perf_counter() - t0
+
+    def step():
+        w = b["work"]
+        for i in range(len(layers)):
+            blk = stream.begin(i)
+            lin(blk["qkv"], w, b["x_qkv"], b["qkv"], out_dtype=f16, split_rows=split)
+            lin(blk["to_out"], w, b["x_out"], b["y"], out_dtype=f16, split_rows=split)
+            lin(blk["mlp_up"], w, b["x_mlp"], b["h"], out_dtype=f16, gelu=True, split_rows=split)
+            lin(blk["mlp_down"], w, b["h"], b["y"], out_dtype=f16, split_rows=split)
+            stream.end(i)
+
+    times = []
+    for _ in range(steps + 1):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        step()
+        e1.record()
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1))
+    ms = sum(times[1:]) / steps
+    gb = stream.block_bytes * len(layers) / 1e9
+    del stream
+    return {"workload": f"the same {len(layers)} blocks streamed from pinned host memory through two device slots",
+            "ms_per_step": round(ms, 3), "first_step_ms": round(times[0], 3), "GB_per_step": round(gb, 2),
+            "host_to_device_GB_s": round(gb / (ms * 1e-3), 1), "pinning_s": round(pin_s, 1)}
 
 
 def _stack_prefix_variant(q, layers, g, steps):

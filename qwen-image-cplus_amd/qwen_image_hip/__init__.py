@@ -11,3 +11,4 @@ from . import ops  # noqa: F401
 from .linear import (SCHEME_W4A16, SCHEME_W4A4_H256, W4A4_FP6, W4A4_INT8, PackedLinear, Work,  # noqa: F401
                      linear)
 from . import qipack  # noqa: F401
+from .stream import BlockStream  # noqa: F401
