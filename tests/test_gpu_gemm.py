@@ -26,8 +26,13 @@ def _h(bits, dev):
 
 
 def _close(got, want):
-    assert rel_l2(got, want) <= REL_L2_TOL, rel_l2(got, want)
-    assert max_abs_over_rms(got, want) <= MAX_ABS_RMS_TOL, max_abs_over_rms(got, want)
+    """Within the north-star tolerance; the measured margin is printed (the
+    GEMV's factored form keeps every weight c * s + min in fp32 instead of
+    rounding it to fp16 first, which shows as a rel-L2 of a few 1e-4)."""
+    e, a = rel_l2(got, want), max_abs_over_rms(got, want)
+    print(f"  rel-L2 {e:.3e} (bar {REL_L2_TOL:g}), max-abs/rms {a:.3e} (bar {MAX_ABS_RMS_TOL:g})", flush=True)
+    assert e <= REL_L2_TOL, e
+    assert a <= MAX_ABS_RMS_TOL, a
 
 
 def _w4a4_case(m, n, k, seed):
