@@ -46,7 +46,7 @@ extern "C" {
 #endif
 
 /* ABI version of this header; bumped on any signature change. */
-#define QI_HIP_ABI_VERSION 3
+#define QI_HIP_ABI_VERSION 4
 int qi_hip_abi_version(void);
 
 /* ---------------------------------------------------------------------------
@@ -148,6 +148,28 @@ int qi_hip_w4a16_gemm_tiled_parts(const void *x_half, const void *w_tiled_codes,
 int qi_hip_w4a16_gemm_tiled_dual(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
                                  const float *bias, void *y, int out_type, int epilogue, int m, int m_split, int n,
                                  int k, int n_part, void *stream);
+
+/* The tiled W4A16 GEMM with a caller workspace: m_split == 0 is
+ * qi_hip_w4a16_gemm_tiled_parts (n outputs), m_split > 0 is
+ * qi_hip_w4a16_gemm_tiled_dual (n outputs per stream, 2n weight rows).
+ * Where few output tiles would leave most CUs walking all of K alone
+ * (short m: the text stream, an encoder's prompt rows), the call splits K
+ * over workgroups: fp32 partial tiles go to the workspace, and a second
+ * kernel adds them in a fixed order (so results do not depend on timing)
+ * and applies the epilogue.  Outputs agree with the workspace-free entries
+ * within the W4A16 tolerance (bit for bit when no split is chosen).
+ * workspace: 16-byte aligned device memory of workspace_bytes, used only
+ * while the call's kernels run on `stream` (calls on one stream may share
+ * it); with less than qi_hip_w4a16_workspace_bytes(m, m_split, n, k) the
+ * call runs unsplit.  No counterpart in the reference, whose one W4A16
+ * kernel has a fixed tile and no K split (gemm.cu:191-268). */
+int qi_hip_w4a16_gemm_tiled_ws(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
+                               const float *bias, void *y, int out_type, int epilogue, int m, int m_split, int n,
+                               int k, int n_part, void *workspace, long long workspace_bytes, void *stream);
+/* Workspace bytes the call above uses for (m, m_split, n, k); 0 when it
+ * splits no K (or the arguments are invalid).  A query only: no device
+ * work. */
+long long qi_hip_w4a16_workspace_bytes(int m, int m_split, int n, int k);
 
 /* The kernel shape the W4A16 GEMMs above choose for m rows and n_out
  * outputs per stream: 0 GEMV (m <= 16), 1 K-split 64 x 64 tiles, 3 tiled

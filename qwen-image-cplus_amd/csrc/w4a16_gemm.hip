@@ -272,12 +272,12 @@ __device__ __forceinline__ void w4a16_group_mfma(const uint8_t *xs, const v2i (&
 // Dequantisation uses packed fp16 (two weights per instruction) when that is
 // provably the reference's value for the group's (scale, minimum), and the
 // reference's fp32 fma + RNE otherwise.
-template <int TM, int TN, int NW>
+template <int TM, int TN, int NW, int NSTAGE>
 __global__ __launch_bounds__(NW *WAVE, (NW >= 8 ? 1 : 2)) void w4a16_tiled_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
     const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int m, int n, int k, int n_part,
     OutMap out, TileGrid2 gd) {
-    constexpr int NSTAGE = 4;
+    static_assert((NSTAGE - 2) * (TM * 2 / NW + 2 * TN) <= 63, "vmcnt range");
     constexpr int BM = TM * 16, BN = NW * TN * 16;
     constexpr int A_INSTR = BM / 8;  // 1 KiB = 8 rows x 128 bytes per direct load
     static_assert(A_INSTR % NW == 0, "loader mapping");
@@ -286,6 +286,9 @@ __global__ __launch_bounds__(NW *WAVE, (NW >= 8 ? 1 : 2)) void w4a16_tiled_kerne
     __shared__ __attribute__((aligned(1024))) uint8_t lds_a[NSTAGE][BM][128];
 
     const int groups = k >> 6;
+    // K split over gridDim.y: this workgroup's groups [g_lo, g_lo + g_cnt).
+    const int g_lo = static_cast<int>(blockIdx.y * groups / gridDim.y);
+    const int g_cnt = static_cast<int>((blockIdx.y + 1) * groups / gridDim.y) - g_lo;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
     const int q = lane >> 4, r16 = lane & 15;
     int tm, tn;
@@ -350,10 +353,10 @@ __global__ __launch_bounds__(NW *WAVE, (NW >= 8 ? 1 : 2)) void w4a16_tiled_kerne
     // (the next tile or row, or zeros past the end) into slots that are never
     // consumed, and keep the number of loads in flight per group constant.
 #pragma unroll
-    for (int p = 0; p < NSTAGE - 1; ++p) issue(p, p);
+    for (int p = 0; p < NSTAGE - 1; ++p) issue(g_lo + p, p);
 
     // Main loop, unrolled by the ring length so ring indices are constants.
-    for (int g0 = 0; g0 < groups; g0 += NSTAGE) {
+    for (int g0 = 0; g0 < g_cnt; g0 += NSTAGE) {
 #pragma unroll
         for (int u = 0; u < NSTAGE; ++u) {
             const int g = g0 + u;
@@ -361,11 +364,15 @@ __global__ __launch_bounds__(NW *WAVE, (NW >= 8 ? 1 : 2)) void w4a16_tiled_kerne
             // later groups' loads remain in flight.
             asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTAGE - 2) * LOADS_PER_GROUP) : "memory");
             __syncthreads();
-            issue(g + NSTAGE - 1, (u + NSTAGE - 1) % NSTAGE);
-            if (g < groups) compute(u);
+            issue(g_lo + g + NSTAGE - 1, (u + NSTAGE - 1) % NSTAGE);
+            if (g < g_cnt) compute(u);
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // A K split writes its raw fp32 partial tile to slice blockIdx.y of the
+    // workspace (the host passes y = workspace, fp32, no epilogue, plain
+    // [m, n] map); w4a16_splitk_reduce adds the slices.
+    if (gridDim.y > 1) y = reinterpret_cast<float *>(y) + static_cast<size_t>(blockIdx.y) * m * n;
 
     // acc[j][i][r] = y[row, col]: row = m-tile i, lane r16; col = this wave's
     // n-tile j, 4q + r.
@@ -395,10 +402,59 @@ __global__ __launch_bounds__(NW *WAVE, (NW >= 8 ? 1 : 2)) void w4a16_tiled_kerne
     }
 }
 
-template <int TM, int TN, int NW>
+// The K-split reduction: y = epilogue(sum over s = 0 .. splits - 1, in that
+// order, of ws[s][row][col]) written through the output map.  Four
+// consecutive outputs per thread.
+__global__ __launch_bounds__(256) void w4a16_splitk_reduce_kernel(const float *__restrict__ ws, int splits,
+                                                                   const float *__restrict__ bias,
+                                                                   void *__restrict__ y, int out_type, int epi, int m,
+                                                                   int n, int n_part, OutMap out) {
+    const long long t = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int n4 = n >> 2;
+    if (t >= static_cast<long long>(m) * n4) return;
+    const int row = static_cast<int>(t / n4), col = static_cast<int>(t % n4) * 4;
+    const size_t plane = static_cast<size_t>(m) * n;
+    const float4 *p = reinterpret_cast<const float4 *>(ws + static_cast<size_t>(row) * n + col);
+    float4 a = p[0];
+    for (int s = 1; s < splits; ++s) {
+        const float4 b = p[s * (plane / 4)];
+        a.x += b.x;
+        a.y += b.y;
+        a.z += b.z;
+        a.w += b.w;
+    }
+    float v[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = epilogue(v[r], bias, col + r, epi);
+    // The parts layout (n_part divides n and is a multiple of 16, so the
+    // four outputs lie in one part).
+    const int part = col / n_part;
+    const size_t idx = static_cast<size_t>(part) * out.m_out * n_part +
+                       static_cast<size_t>(out.row_base + row) * n_part + (col - part * n_part);
+    if (out_type == QI_HIP_OUT_F16) {
+        uint2 h;
+        h.x = static_cast<uint32_t>(f2h(v[0])) | (static_cast<uint32_t>(f2h(v[1])) << 16);
+        h.y = static_cast<uint32_t>(f2h(v[2])) | (static_cast<uint32_t>(f2h(v[3])) << 16);
+        *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(y) + idx) = h;
+    } else {
+        *reinterpret_cast<float4 *>(reinterpret_cast<float *>(y) + idx) = float4{v[0], v[1], v[2], v[3]};
+    }
+}
+
+static int launch_splitk_reduce(const float *ws, int splits, const float *bias, void *y, int out_type, int epi,
+                                int m, int n, int n_part, OutMap out, hipStream_t stream) {
+    const long long threads = static_cast<long long>(m) * (n / 4);
+    const long long blocks = (threads + 255) / 256;
+    if (blocks > 0x7FFFFFFFLL) return kInvalid;
+    w4a16_splitk_reduce_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(
+        ws, splits, bias, y, out_type, epi, m, n, n_part, out);
+    return launch_status();
+}
+
+template <int TM, int TN, int NW, int NSTAGE = 4>
 static int launch_tiled(const void *x, const void *codes, const void *scales, const float *bias, void *y,
                         int out_type, int epi, int m, int n, int k, int n_part, OutMap out, int m_split,
-                        hipStream_t stream) {
+                        hipStream_t stream, int splits = 1, float *ws = nullptr) {
     constexpr int BM = TM * 16, BN = NW * TN * 16;
     // One grid (m_split = 0), or the two streams' diagonal blocks (m_split
     // and out.n_out multiples of BM and BN, checked by the caller).
@@ -410,7 +466,17 @@ static int launch_tiled(const void *x, const void *codes, const void *scales, co
         gd = TileGrid2{((m + BM - 1) / BM) * ((n + BN - 1) / BN), (m + BM - 1) / BM, (n + BN - 1) / BN, 0, 0};
     const long long blocks = static_cast<long long>(gd.t0) + static_cast<long long>(gd.tm1) * gd.tn1;
     if (blocks > 0x7FFFFFFFLL) return kInvalid;
-    w4a16_tiled_kernel<TM, TN, NW><<<dim3(static_cast<unsigned>(blocks)), dim3(NW * WAVE), 0, stream>>>(
+    if (splits > 1) {
+        // Partials into the workspace, then one reduction with the epilogue.
+        w4a16_tiled_kernel<TM, TN, NW, NSTAGE>
+            <<<dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(splits)), dim3(NW * WAVE), 0, stream>>>(
+                static_cast<const uint16_t *>(x), static_cast<const uint8_t *>(codes),
+                static_cast<const uint16_t *>(scales), nullptr, ws, QI_HIP_OUT_F32, QI_HIP_EPILOGUE_NONE, m, n, k, n,
+                OutMap{0, m, n}, gd);
+        if (const int st = launch_status()) return st;
+        return launch_splitk_reduce(ws, splits, bias, y, out_type, epi, m, n, n_part, out, stream);
+    }
+    w4a16_tiled_kernel<TM, TN, NW, NSTAGE><<<dim3(static_cast<unsigned>(blocks)), dim3(NW * WAVE), 0, stream>>>(
         static_cast<const uint16_t *>(x), static_cast<const uint8_t *>(codes), static_cast<const uint16_t *>(scales),
         bias, y, out_type, epi, m, n, k, n_part, out, gd);
     return launch_status();
@@ -630,40 +696,88 @@ static int select_w4a16_tiles(int m, int n_out) {
     return 6;
 }
 
+// K split over workgroups for a single-stream launch of m rows and n_out
+// outputs (1 = none).  Few 64 x 64 tiles leave most CUs with one wave per
+// SIMD walking all of K, which is latency-bound; splitting K into s slices
+// (their fp32 partials added by a second, small kernel in slice order)
+// multiplies the workgroups.  s brings the workgroups to about three per CU
+// with at least 16 groups per slice; where the in-workgroup K split (tile
+// choice 1) runs, only for long K (>= 96 groups), where it measured slower.
+// Measured on MI355X (us, unsplit -> split): 300 x 1024 x 3584 23.5 ->
+// 14.8 (s = 3), 300 x 3584 x 3584 28.7 -> 26.3 (3), 300 x 3584 x 18944
+// 109 -> 78 (3), 512 x 3072 x 12288 75.5 -> 64.6 (2), 512 x 1024 x 3072
+// 20.9 -> 15.7 (3), 256 x 3072 x 12288 51.9 -> 37.5 (4), 64 x 3072 x 12288
+// 48.6 -> 20.7 (12); 256 x 3072 x 3072 stays on choice 1 (18.5 against 21.0
+// split).
+static int select_w4a16_splits(int m, int n_out, int k) {
+    const int cfg = select_w4a16_tiles(m, n_out);
+    if (cfg != 1 && cfg != 3) return 1;
+    const long long tiles = static_cast<long long>((m + 63) / 64) * ((n_out + 63) / 64);
+    const int groups = k / 64;
+    if (tiles >= 512 || (cfg == 1 && groups < 96)) return 1;
+    const long long want = (3LL * device_cus() + tiles - 1) / tiles;
+    const int s = static_cast<int>(want < groups / 16 ? want : groups / 16);
+    return s > 1 ? s : 1;
+}
+
+static size_t splitk_bytes(int m, int n_out, int k) {
+    const int s = select_w4a16_splits(m, n_out, k);
+    return s > 1 ? static_cast<size_t>(s) * m * n_out * 4 : 0;
+}
+
+static const int kTileRows[] = {0, 64, 32, 64, 128, 256, 128}, kTileCols[] = {0, 64, 64, 64, 192, 256, 128};
+
+// One launch over both streams (m_split > 0) only when its tiles fit both
+// blocks and it takes no more rounds of workgroups than stream 0 alone
+// (these kernels are not persistent: stream 1's tiles would otherwise run
+// as an extra, mostly idle round).
+static bool w4a16_one_launch(int cfg, int m, int m_split, int n_out) {
+    const int bm = kTileRows[cfg], bn = kTileCols[cfg];
+    if (m_split <= 0 || cfg == 1 || m_split % bm || n_out % bn) return false;
+    const long long slots = static_cast<long long>(device_cus()) * (cfg == 5 ? 1 : 2);
+    const long long t0 = static_cast<long long>(m_split / bm) * (n_out / bn);
+    const long long t1 = static_cast<long long>((m - m_split + bm - 1) / bm) * (n_out / bn);
+    return (t0 + t1 + slots - 1) / slots == (t0 + slots - 1) / slots;
+}
+
+// Workspace a call needs for its K splits (0: none).  A dual call split
+// into two launches runs them in stream order, so they share it.
+static size_t w4a16_workspace(int m, int m_split, int n_out, int k) {
+    if (m_split <= 0) return splitk_bytes(m, n_out, k);
+    if (w4a16_one_launch(select_w4a16_tiles(m, n_out), m, m_split, n_out)) return 0;
+    const size_t a = splitk_bytes(m_split, n_out, k), b = splitk_bytes(m - m_split, n_out, k);
+    return a > b ? a : b;
+}
+
 // Kernel shape for m rows and n_out outputs per stream (measured on
 // MI355X), and its launch.  m_split = 0: one stream (n = n_out).  m_split >
 // 0: the two streams' diagonal blocks over the stacked rows (n = 2 n_out
 // weight rows) in one launch when the chosen tiles fit both blocks, else
-// one launch per stream.  Arguments are checked by the callers; m > 16 per
-// stream.
+// one launch per stream.  ws (ws_bytes) is the caller's workspace for K
+// splits, or null: without it no launch splits K.  Arguments are checked by
+// the callers; m > 16 per stream.
 static int dispatch_w4a16(const void *x, const void *codes, const void *scales, const float *bias, void *y,
                           int out_type, int epi, int m, int n, int k, int n_part, OutMap out, int m_split,
-                          hipStream_t s) {
+                          hipStream_t s, float *ws, size_t ws_bytes) {
     const int n_out = out.n_out;
     const int cfg = select_w4a16_tiles(m, n_out);
-    const int bm[] = {0, 64, 32, 64, 128, 256, 128}, bn[] = {0, 64, 64, 64, 192, 256, 128};
-    // One launch over both streams only when its tiles fit both blocks and
-    // it takes no more rounds of workgroups than stream 0 alone (these
-    // kernels are not persistent: stream 1's tiles would otherwise run as an
-    // extra, mostly idle round).
-    bool one_launch = m_split > 0 && cfg != 1 && m_split % bm[cfg] == 0 && n_out % bn[cfg] == 0;
-    if (one_launch) {
-        const long long slots = static_cast<long long>(device_cus()) * (cfg == 5 ? 1 : 2);
-        const long long t0 = static_cast<long long>(m_split / bm[cfg]) * (n_out / bn[cfg]);
-        const long long t1 = static_cast<long long>((m - m_split + bm[cfg] - 1) / bm[cfg]) * (n_out / bn[cfg]);
-        one_launch = (t0 + t1 + slots - 1) / slots == (t0 + slots - 1) / slots;
-    }
-    if (m_split > 0 && !one_launch) {
+    if (m_split > 0 && !w4a16_one_launch(cfg, m, m_split, n_out)) {
         // One launch per stream, each writing its rows of the stacked y.
         const size_t g = static_cast<size_t>(k / 64);
         int st = dispatch_w4a16(x, codes, scales, bias, y, out_type, epi, m_split, n_out, k, n_part,
-                                OutMap{out.row_base, out.m_out, n_out}, 0, s);
+                                OutMap{out.row_base, out.m_out, n_out}, 0, s, ws, ws_bytes);
         if (st) return st;
         return dispatch_w4a16(static_cast<const uint16_t *>(x) + static_cast<size_t>(m_split) * k,
                               static_cast<const uint8_t *>(codes) + static_cast<size_t>(n_out / 16) * g * 512,
                               static_cast<const uint8_t *>(scales) + static_cast<size_t>(n_out / 16) * g * 64,
                               bias ? bias + n_out : nullptr, y, out_type, epi, m - m_split, n_out, k, n_part,
-                              OutMap{out.row_base + m_split, out.m_out, n_out}, 0, s);
+                              OutMap{out.row_base + m_split, out.m_out, n_out}, 0, s, ws, ws_bytes);
+    }
+    if (m_split == 0 && ws) {
+        const int splits = select_w4a16_splits(m, n_out, k);
+        if (splits > 1 && static_cast<size_t>(splits) * m * n * 4 <= ws_bytes)
+            return launch_tiled<4, 1, 4>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, 0, s,
+                                         splits, ws);
     }
     switch (cfg) {
     case 1:
@@ -694,32 +808,48 @@ static int check_w4a16_args(const void *x_half, const void *w_tiled_codes, const
 
 }  // namespace qi
 
-QI_API int qi_hip_w4a16_gemm_tiled_parts(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
-                                         const float *bias, void *y, int out_type, int epilogue, int m, int n, int k,
-                                         int n_part, void *stream) {
+namespace qi {
+
+// Every tiled W4A16 entry: m_split = 0 one stream of n outputs, else the two
+// streams of a dual call (n outputs each, 2n weight rows).
+static int w4a16_entry(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales, const float *bias,
+                       void *y, int out_type, int epilogue, int m, int m_split, int n, int k, int n_part,
+                       void *workspace, long long workspace_bytes, void *stream) {
     if (const int st = check_w4a16_args(x_half, w_tiled_codes, w_tiled_scales, y, out_type, epilogue, m, n, k, n_part))
         return st;
-    if (m <= 16)
+    if (workspace_bytes < 0 || (workspace_bytes > 0 && (!workspace || reinterpret_cast<uintptr_t>(workspace) % 16)))
+        return kInvalid;
+    const int rows = m_split > 0 ? 2 * n : n;
+    if (static_cast<long long>(m) * k * 2 >= (1LL << 32) || static_cast<long long>(rows) * (k / 2) >= (1LL << 32))
+        return kInvalid;
+    if (m_split > 0) {
+        if (m_split <= 16 || m - m_split <= 16) return kInvalid;
+    } else if (m <= 16) {
         // The GEMV writes the parts layout itself: one launch over all parts
         // (e.g. every block's modulation linears, which share their input).
         return qi_hip_w4a16_gemv_impl(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
                                       n_part, stream_of(stream));
-    if (static_cast<long long>(m) * k * 2 >= (1LL << 32) || static_cast<long long>(n) * (k / 2) >= (1LL << 32))
-        return kInvalid;
-    return dispatch_w4a16(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k, n_part,
-                          OutMap{0, m, n}, 0, stream_of(stream));
+    }
+    return dispatch_w4a16(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, rows, k, n_part,
+                          OutMap{0, m, n}, m_split, stream_of(stream), static_cast<float *>(workspace),
+                          static_cast<size_t>(workspace_bytes));
+}
+
+}  // namespace qi
+
+QI_API int qi_hip_w4a16_gemm_tiled_parts(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
+                                         const float *bias, void *y, int out_type, int epilogue, int m, int n, int k,
+                                         int n_part, void *stream) {
+    return w4a16_entry(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, 0, n, k, n_part,
+                       nullptr, 0, stream);
 }
 
 QI_API int qi_hip_w4a16_gemm_tiled_dual(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
                                         const float *bias, void *y, int out_type, int epilogue, int m, int m_split,
                                         int n, int k, int n_part, void *stream) {
-    if (const int st = check_w4a16_args(x_half, w_tiled_codes, w_tiled_scales, y, out_type, epilogue, m, n, k, n_part))
-        return st;
-    if (m_split <= 16 || m - m_split <= 16) return kInvalid;
-    if (static_cast<long long>(m) * k * 2 >= (1LL << 32) || static_cast<long long>(2 * n) * (k / 2) >= (1LL << 32))
-        return kInvalid;
-    return dispatch_w4a16(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, 2 * n, k, n_part,
-                          OutMap{0, m, n}, m_split, stream_of(stream));
+    if (m_split <= 0) return kInvalid;
+    return w4a16_entry(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, m_split, n, k, n_part,
+                       nullptr, 0, stream);
 }
 
 QI_API int qi_hip_w4a16_gemm_tiled(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
@@ -727,6 +857,21 @@ QI_API int qi_hip_w4a16_gemm_tiled(const void *x_half, const void *w_tiled_codes
                                    void *stream) {
     return qi_hip_w4a16_gemm_tiled_parts(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, n, k,
                                          n, stream);
+}
+
+QI_API long long qi_hip_w4a16_workspace_bytes(int m, int m_split, int n, int k) {
+    if (m <= 16 || n <= 0 || k <= 0 || n % 16 || k % 64 || m_split < 0 || m_split >= m) return 0;
+    if (m_split > 0 && (m_split <= 16 || m - m_split <= 16)) return 0;
+    return static_cast<long long>(w4a16_workspace(m, m_split, n, k));
+}
+
+QI_API int qi_hip_w4a16_gemm_tiled_ws(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
+                                      const float *bias, void *y, int out_type, int epilogue, int m, int m_split,
+                                      int n, int k, int n_part, void *workspace, long long workspace_bytes,
+                                      void *stream) {
+    if (m_split < 0) return kInvalid;
+    return w4a16_entry(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, epilogue, m, m_split, n, k, n_part,
+                       workspace, workspace_bytes, stream);
 }
 
 QI_API int qi_hip_w4a16_tiles(int m, int n_out) {

@@ -41,6 +41,7 @@ SIGNATURES: dict[str, list] = {
     "qi_hip_w4a16_gemm_tiled_parts": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p],
     "qi_hip_w4a16_gemm_tiled_dual": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p],
     "qi_hip_w4a16_tiles": [_i, _i],
+    "qi_hip_w4a16_gemm_tiled_ws": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p, ctypes.c_longlong, _p],
     "qi_hip_w4a4_fp6_tiles": [_i, _i],
     "qi_flash_attention": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
     "qi_hip_flash_attention": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p],
@@ -58,9 +59,10 @@ SIGNATURES: dict[str, list] = {
     "qi_pack_verify": [_p, _i],
 }
 # Entry points whose return type is not int.
-RESTYPES = {"qi_fnv1a": (_u64, [_u64, _p, _u64]), "qi_pack_close": (None, [_p])}
+RESTYPES = {"qi_fnv1a": (_u64, [_u64, _p, _u64]), "qi_pack_close": (None, [_p]),
+            "qi_hip_w4a16_workspace_bytes": (ctypes.c_longlong, [_i, _i, _i, _i])}
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lib = None
 

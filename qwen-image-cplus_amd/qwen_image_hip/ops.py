@@ -174,34 +174,56 @@ def _out_shape(m: int, n: int, n_part: int | None):
     return (n // n_part, m, n_part)
 
 
+def _w4a16_call(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, gelu, m, m_split, n, k, n_part,
+                split_k):
+    lib = load()
+    epi = EPILOGUE_GELU_TANH if gelu else EPILOGUE_NONE
+    n_part = n if n_part is None else n_part
+    if not split_k:
+        if m_split:
+            return lib.qi_hip_w4a16_gemm_tiled_dual(_ptr(x_half), _ptr(w_tiled_codes), _ptr(w_tiled_scales),
+                                                    _ptr(bias), _ptr(y), out_type, epi, m, m_split, n, k, n_part,
+                                                    _stream())
+        return lib.qi_hip_w4a16_gemm_tiled_parts(_ptr(x_half), _ptr(w_tiled_codes), _ptr(w_tiled_scales), _ptr(bias),
+                                                 _ptr(y), out_type, epi, m, n, k, n_part, _stream())
+    # The K-split workspace comes from torch's caching allocator on the
+    # current stream (so it is also valid under graph capture).
+    ws_bytes = lib.qi_hip_w4a16_workspace_bytes(m, m_split, n, k)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=x_half.device) if ws_bytes > 0 else None
+    return lib.qi_hip_w4a16_gemm_tiled_ws(_ptr(x_half), _ptr(w_tiled_codes), _ptr(w_tiled_scales), _ptr(bias),
+                                          _ptr(y), out_type, epi, m, m_split, n, k, n_part, _ptr(ws), ws_bytes,
+                                          _stream())
+
+
 def w4a16_gemm(x_half, w_tiled_codes, w_tiled_scales, bias=None, out_dtype=torch.float32, gelu=False, y=None,
-               n_part=None):
+               n_part=None, split_k=True):
     """y = x . W^T for tiled W4A16 weights; with n_part, y is [n / n_part, m, n_part]
-    (the parts of a fused record, qi_hip_w4a16_gemm_tiled_parts)."""
+    (the parts of a fused record).  split_k: qi_hip_w4a16_gemm_tiled_ws with a
+    workspace (K split over workgroups where the library chooses one), else
+    qi_hip_w4a16_gemm_tiled_parts."""
     m, k = x_half.shape
     n = w_tiled_codes.shape[0]
     out_type = OUT_F16 if out_dtype == torch.float16 else OUT_F32
     y = y if y is not None else _empty(_out_shape(m, n, n_part), out_dtype, x_half)
-    st = load().qi_hip_w4a16_gemm_tiled_parts(_ptr(x_half), _ptr(w_tiled_codes), _ptr(w_tiled_scales), _ptr(bias),
-                                              _ptr(y), out_type, EPILOGUE_GELU_TANH if gelu else EPILOGUE_NONE, m, n,
-                                              k, n if n_part is None else n_part, _stream())
-    check(st, "w4a16 gemm")
+    check(_w4a16_call(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, gelu, m, 0, n, k, n_part, split_k),
+          "w4a16 gemm")
     return y
 
 
 def w4a16_gemm_dual(x_half, w_tiled_codes, w_tiled_scales, m_split: int, bias=None, out_dtype=torch.float32,
-                    gelu=False, y=None, n_part=None):
-    """Both streams of a dual-stream block (qi_hip_w4a16_gemm_tiled_dual):
-    rows < m_split use the first half of the weight rows, the others the
-    second; y is [m, n] (or [n / n_part, m, n_part]), n = weight rows / 2."""
+                    gelu=False, y=None, n_part=None, split_k=True):
+    """Both streams of a dual-stream block: rows < m_split use the first half
+    of the weight rows, the others the second; y is [m, n] (or [n / n_part,
+    m, n_part]), n = weight rows / 2.  split_k as in w4a16_gemm (else
+    qi_hip_w4a16_gemm_tiled_dual)."""
     m, k = x_half.shape
     n = w_tiled_codes.shape[0] // 2
+    if m_split <= 0:
+        raise ValueError("m_split must be positive")
     out_type = OUT_F16 if out_dtype == torch.float16 else OUT_F32
     y = y if y is not None else _empty(_out_shape(m, n, n_part), out_dtype, x_half)
-    st = load().qi_hip_w4a16_gemm_tiled_dual(_ptr(x_half), _ptr(w_tiled_codes), _ptr(w_tiled_scales), _ptr(bias),
-                                             _ptr(y), out_type, EPILOGUE_GELU_TANH if gelu else EPILOGUE_NONE, m,
-                                             m_split, n, k, n if n_part is None else n_part, _stream())
-    check(st, "w4a16 gemm")
+    check(_w4a16_call(x_half, w_tiled_codes, w_tiled_scales, bias, y, out_type, gelu, m, m_split, n, k, n_part,
+                      split_k), "w4a16 gemm")
     return y
 
 

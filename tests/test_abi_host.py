@@ -16,7 +16,7 @@ HEADER = ROOT / "include" / "qwen_image_hip.h"
 
 def declared_functions():
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:int|void|uint64_t)\s+(qi_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|void|uint64_t|long long)\s+(qi_\w+)\s*\(", text, flags=re.M)))
 
 
 def test_header_declares_the_reference_entry_points():
@@ -126,6 +126,35 @@ def test_w4a16_tile_choice(m, n_out, cfg):
 ])
 def test_fp6_tile_choice(m, n, cfg):
     assert qwen_image_hip.load().qi_hip_w4a4_fp6_tiles(m, n) == cfg
+
+
+@pytest.mark.parametrize("m,m_split,n,k,slices", [
+    (300, 0, 1024, 3584, 3), (300, 0, 3584, 3584, 3), (300, 0, 3584, 18944, 3), (300, 0, 37888, 3584, 0),
+    (256, 0, 3072, 12288, 4), (256, 0, 3072, 3072, 0), (64, 0, 3072, 12288, 12), (512, 0, 3072, 12288, 2),
+    (4096, 0, 3072, 3072, 0), (4096, 0, 12288, 3072, 0), (16, 0, 3072, 12288, 0),
+])
+def test_w4a16_split_choice(m, m_split, n, k, slices):
+    """K slices the W4A16 call with a workspace chooses (workspace bytes =
+    slices * m * n * 4), at a 256-CU device's rule (the library's default
+    when no GPU is visible)."""
+    assert qwen_image_hip.load().qi_hip_w4a16_workspace_bytes(m, m_split, n, k) == slices * m * n * 4
+
+
+def test_w4a16_split_choice_dual():
+    """A dual call run as two launches needs the larger stream's workspace;
+    one launch over both streams splits nothing."""
+    L = qwen_image_hip.load()
+    assert L.qi_hip_w4a16_workspace_bytes(4352, 4096, 3072, 12288) == 4 * 256 * 3072 * 4
+    assert L.qi_hip_w4a16_workspace_bytes(4352, 4096, 9216, 3072) == 0
+    assert L.qi_hip_w4a16_workspace_bytes(4352, 4352, 3072, 3072) == 0  # invalid m_split
+
+
+def test_w4a16_ws_entry_checks():
+    L = qwen_image_hip.load()
+    # negative workspace size, unaligned workspace, negative m_split
+    assert L.qi_hip_w4a16_gemm_tiled_ws(16, 16, 16, None, 16, 0, 0, 64, 0, 64, 64, 64, 16, -1, None) == INVALID
+    assert L.qi_hip_w4a16_gemm_tiled_ws(16, 16, 16, None, 16, 0, 0, 64, 0, 64, 64, 64, 8, 64, None) == INVALID
+    assert L.qi_hip_w4a16_gemm_tiled_ws(16, 16, 16, None, 16, 0, 0, 64, -1, 64, 64, 64, 16, 64, None) == INVALID
 
 
 def test_tile_queries_reject_empty_shapes():
