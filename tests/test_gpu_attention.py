@@ -30,14 +30,35 @@ def _run(dev, q, k, v, heads, **kw):
 
 
 def _close(got, want):
-    assert rel_l2(got, want) <= REL_L2_TOL, rel_l2(got, want)
-    assert max_abs_over_rms(got, want) <= MAX_ABS_RMS_TOL, max_abs_over_rms(got, want)
+    e, a = rel_l2(got, want), max_abs_over_rms(got, want)
+    print(f"  rel-L2 {e:.3e} (bar {REL_L2_TOL:g}), max-abs/rms {a:.3e} (bar {MAX_ABS_RMS_TOL:g})", flush=True)
+    assert e <= REL_L2_TOL, e
+    assert a <= MAX_ABS_RMS_TOL, a
 
 
 @pytest.mark.parametrize("nq,nk,heads", [(1, 64, 1), (200, 300, 3), (129, 1000, 2)])
 def test_attention_unmasked(dev, nq, nk, heads):
     print(f"attention nq={nq} nk={nk} heads={heads}", flush=True)
     q, k, v = _case(nq, nk, heads, 1000 + nq)
+    _close(_run(dev, q, k, v, heads), oracle.flash_attention(q, k, v, heads))
+
+
+@pytest.mark.parametrize("step", [0.05, 0.5, 3.0])
+def test_attention_rising_scores(dev, step):
+    """Scores that rise from key tile to key tile (by `step` per key in the
+    log2 domain, so the running maximum grows by less than, about, and far
+    more than the kernel's rescaling threshold per 64-key tile), against
+    the oracle."""
+    rng = np.random.default_rng(1400)
+    nq, nk, heads = 96, 700, 1
+    u = rng.normal(0, 1, size=128).astype(np.float32)
+    u /= np.linalg.norm(u)
+    # q_i . k_j ~ 3 c_j + noise; in the kernel's log2 domain (scale
+    # log2(e) / sqrt(128)) the score of key j is about step * j.
+    c = step * np.arange(nk, dtype=np.float32) / (3.0 * 1.4426950408889634 / np.sqrt(128.0))
+    q = (rng.normal(0, 0.3, size=(nq, 128)) + 3.0 * u).astype(np.float32)
+    k = oracle.half_from_f32((rng.normal(0, 0.3, size=(nk, 128)) + c[:, None] * u).astype(np.float32))
+    v = oracle.half_from_f32(rng.normal(0, 1, size=(nk, 128)).astype(np.float32))
     _close(_run(dev, q, k, v, heads), oracle.flash_attention(q, k, v, heads))
 
 
