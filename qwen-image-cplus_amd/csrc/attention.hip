@@ -183,17 +183,30 @@ __global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_kernel(
         const uint16_t *vt_lds = vt_lds2[buf];
 
         // S^T for the tile's two 32-key halves t: register 4a + b of s[t]
-        // holds key start + 32t + 8a + 4h + b of the lane's query.
+        // holds key start + 32t + 8a + 4h + b of the lane's query.  The two
+        // halves' MFMA chains alternate (step f: dims 16 (f / 2), half f % 2)
+        // and each K fragment is read KLA steps ahead of its MFMA.
         v16f_t s[2];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r) s[t][r] = 0.f;
-            const uint16_t *krow = k_lds + (32 * t + l32) * ATT_KROW + 8 * h;
+        {
+            constexpr int KLA = 4;
+            v8h_t kf[16];
+            auto read_k = [&](int f) {
+                kf[f] = *reinterpret_cast<const v8h_t *>(k_lds + (32 * (f & 1) + l32) * ATT_KROW + 8 * h +
+                                                         16 * (f >> 1));
+            };
 #pragma unroll
-            for (int st = 0; st < 8; ++st)
-                s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const v8h_t *>(krow + 16 * st), qf[st],
-                                                             s[t], 0, 0, 0);
+            for (int f = 0; f < KLA; ++f) read_k(f);
+#pragma unroll
+            for (int f = 0; f < 16; ++f) {
+                if (f + KLA < 16) read_k(f + KLA);
+                __builtin_amdgcn_sched_barrier(0);
+                s[f & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[f], qf[f >> 1], s[f & 1], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
         // Mask, row max (this lane's 32 keys, then the other half's).
         if (start + ATT_KT > wmin) {
@@ -211,6 +224,17 @@ __global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        constexpr int VLA = 4;
+        v8h_t vf[16];
+        auto read_v = [&](int f) {
+            const uint16_t *vrow = vt_lds + (32 * (f >> 2) + l32) * ATT_VROW + 4 * h + 32 * ((f >> 1) & 1) + 16 * (f & 1);
+            const uint2 lo = *reinterpret_cast<const uint2 *>(vrow);
+            const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + 8);
+            vf[f] = __builtin_bit_cast(v8h_t, uint4{lo.x, lo.y, hi.x, hi.y});
+        };
+#pragma unroll
+        for (int f = 0; f < VLA; ++f) read_v(f);
+        __builtin_amdgcn_sched_barrier(0);
         // The offset moves only when the tile's maximum exceeds it by more
         // than 2^8 (exp2 domain), so O and the sum are rarely rescaled: the
         // probabilities stay <= 256, exact in fp16's normal range as
@@ -244,19 +268,16 @@ __global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_kernel(
         m_run = new_m;
         // O^T += V^T P^T.  Step (t, e) covers keys 32t + 16e + 8(i / 4) +
         // 4h + i % 4 in K slot 8h + i: from the V^T row of dim d, the runs
-        // of 4 keys at 32t + 16e + 4h and 32t + 16e + 8 + 4h.
+        // of 4 keys at 32t + 16e + 4h and 32t + 16e + 8 + 4h.  MFMA f = 4j
+        // + 2t + e; its V fragment is read VLA MFMAs ahead (the first ones
+        // before the softmax, above).
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint16_t *vrow = vt_lds + (32 * j + l32) * ATT_VROW + 4 * h;
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const uint2 lo = *reinterpret_cast<const uint2 *>(vrow + 32 * t + 16 * e);
-                    const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + 32 * t + 16 * e + 8);
-                    const v8h_t a = __builtin_bit_cast(v8h_t, uint4{lo.x, lo.y, hi.x, hi.y});
-                    o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[t][e], o[j], 0, 0, 0);
-                }
+        for (int f = 0; f < 16; ++f) {
+            if (f + VLA < 16) read_v(f + VLA);
+            __builtin_amdgcn_sched_barrier(0);
+            const int j = f >> 2, t = (f >> 1) & 1, e = f & 1;
+            o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[f], pb[t][e], o[j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
         if (start + ATT_KT < limit) store_tile(buf ^ 1);
         __syncthreads();
