@@ -907,7 +907,7 @@ def cpu_baseline_gemv(reps=5):
     return out
 
 
-ABLATION_NAMES = ("none", "dma", "lds", "barrier", "fma", "mfma", "memory", "arith_only")
+ABLATION_NAMES = ("none", "dma", "lds", "barrier", "vmwait", "fma", "mfma", "memory", "arith_only")
 
 
 def ablate_w4a4(iters=20, reps=5):

@@ -125,7 +125,7 @@ def build_probe() -> list[Path]:
 
 
 # name -> QI_ABLATE_* macros of the W4A4 measurement builds.
-ABLATIONS = {"none": (), "dma": ("DMA",), "lds": ("LDS",), "barrier": ("BARRIER",), "fma": ("FMA",),
+ABLATIONS = {"none": (), "dma": ("DMA",), "lds": ("LDS",), "barrier": ("BARRIER",), "vmwait": ("VMWAIT",), "fma": ("FMA",),
              "mfma": ("MFMA",), "memory": ("DMA", "LDS"), "arith_only": ("DMA", "LDS", "BARRIER")}
 
 

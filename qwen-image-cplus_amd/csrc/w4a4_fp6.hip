@@ -42,7 +42,8 @@
 // QI_ABLATE_* macro removes one part of the GEMM's work so that its cost
 // shows as the time saved -- QI_ABLATE_DMA the direct-to-LDS operand loads,
 // QI_ABLATE_LDS the fragment reads after the first group, QI_ABLATE_BARRIER
-// the per-group workgroup barrier, QI_ABLATE_FMA the exact fp32 group steps,
+// the per-group workgroup barrier, QI_ABLATE_VMWAIT the per-group wait for
+// the next group's operand loads, QI_ABLATE_FMA the exact fp32 group steps,
 // QI_ABLATE_MFMA the matrix-core work (partials and scale products).  The
 // product library defines none of them.
 
@@ -344,7 +345,11 @@ __device__ __forceinline__ void fp6_tiles(uint8_t *lds, const uint8_t *__restric
         // __syncthreads' release fence would also wait for the loads of the
         // groups still in flight.
         __builtin_amdgcn_sched_barrier(0);
+#ifdef QI_ABLATE_VMWAIT
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#else
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((NSTAGE - 2) * LOADS_PER_GROUP) : "memory");
+#endif
 #ifndef QI_ABLATE_BARRIER
         __builtin_amdgcn_s_barrier();
 #endif
