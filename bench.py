@@ -795,7 +795,12 @@ PROBE_BODIES = {0: "fp6 MFMA x4 (4 chains)", 1: "fp32 FMA x64", 2: "MFMA x4 + FM
                 5: "body 3 in the product kernel's order (partial tiles two tiles behind their FMAs)",
                 6: "ds_read_b128 x8 (1 KiB per wave each): LDS read throughput",
                 7: "fp32 FMA x64 on 16 accumulators (few registers)",
-                8: "direct-to-LDS loads 4 x 1 KiB per wave (L2-resident): L2 -> LDS throughput"}
+                8: "direct-to-LDS loads 4 x 1 KiB per wave (L2-resident): L2 -> LDS throughput",
+                9: "f32 32x32x1 2-block MFMA x4 (2048 outputs each)",
+                10: "f16 32x32x4 2-block MFMA x4 (2048 outputs each)",
+                11: "f16 32x32x8 MFMA x4 (1024 outputs each)",
+                12: "f16 16x16x4 4-block MFMA x4 (1024 outputs each)",
+                13: "f16 4x4x4 16-block MFMA x4 (256 outputs each)"}
 
 
 def probe_overlap(iters=2000):

@@ -24,6 +24,13 @@
 //      waves per SIMD
 //   8  direct-to-LDS loads, 4 KiB per wave per iteration from an
 //      L2-resident window: L2 -> LDS throughput
+//   9  four independent v_mfma_f32_32x32x1_2b_f32 (the W4A4 kernel's exact
+//      scale outer product: 2048 products each)
+//  10  four independent v_mfma_f32_32x32x4_2b_f16 (2048 outputs each; with
+//      one non-zero K slot, an exact product of two fp16 values)
+//  11  four independent v_mfma_f32_32x32x8_f16 (1024 outputs each)
+//  12  four independent v_mfma_f32_16x16x4_4b_f16 (1024 outputs each)
+//  13  four independent v_mfma_f32_4x4x4_16b_f16 (256 outputs each)
 // and records s_memtime (shader clock) around the loop.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -36,6 +43,8 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 template <typename T>
 __device__ __forceinline__ void opaque(T &v) {
@@ -75,6 +84,8 @@ __global__ __launch_bounds__(256) void probe_kernel(int iters, const int *__rest
     constexpr bool MATRIX = BODY <= 5;  // bodies that use the matrix core
     v16f p[4] = {};
     v32f sp[2] = {};
+    v32f w32[4] = {};
+    v4f w4[4] = {};
     if constexpr (MATRIX) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) p[t] = mfma6(a[t], b);
@@ -193,6 +204,26 @@ __global__ __launch_bounds__(256) void probe_kernel(int iters, const int *__rest
                 v4i v = lds[(r + it) & 7][64 * wv + lane];
                 rd[r] += v;
             }
+        } else if constexpr (BODY >= 9 && BODY <= 13) {
+            // Output-rate of the small-K MFMA shapes (four accumulation
+            // chains; operands made opaque above through a and b).
+            v4h ha[4], hb;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) ha[t] = __builtin_bit_cast(v4h, __builtin_shufflevector(a[t], a[t], 0, 1));
+            hb = __builtin_bit_cast(v4h, __builtin_shufflevector(b, b, 0, 1));
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                if constexpr (BODY == 9)
+                    w32[t] = __builtin_amdgcn_mfma_f32_32x32x1f32(x[t], x[t + 4], w32[t], 0, 0, 0);
+                else if constexpr (BODY == 10)
+                    w32[t] = __builtin_amdgcn_mfma_f32_32x32x4f16(ha[t], hb, w32[t], 0, 0, 0);
+                else if constexpr (BODY == 11)
+                    p[t] = __builtin_amdgcn_mfma_f32_32x32x8f16(ha[t], hb, p[t], 0, 0, 0);
+                else if constexpr (BODY == 12)
+                    p[t] = __builtin_amdgcn_mfma_f32_16x16x4f16(ha[t], hb, p[t], 0, 0, 0);
+                else
+                    w4[t] = __builtin_amdgcn_mfma_f32_4x4x4f16(ha[t], hb, w4[t], 0, 0, 0);
+            }
         } else if constexpr (BODY == 4) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
@@ -223,6 +254,17 @@ __global__ __launch_bounds__(256) void probe_kernel(int iters, const int *__rest
     }
 #pragma unroll
     for (int r = 0; r < 8; ++r) s += static_cast<float>(rd[r][0] + rd[r][1] + rd[r][2] + rd[r][3]);
+    if constexpr (BODY >= 9) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+            for (int r = 0; r < 32; ++r) s += w32[t][r];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s += p[t][r];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s += w4[t][r];
+        }
+    }
     const int gid = blockIdx.x * blockDim.x + threadIdx.x;
     out[gid] = s;
     if (lane == 0) cycles[gid >> 6] = t1 - t0;
@@ -248,6 +290,11 @@ extern "C" __attribute__((visibility("default"))) int qi_probe_run(int body, int
         if (blocks * 256 < 64 * 1024) return static_cast<int>(hipErrorInvalidValue);  // the 256 KiB window
         probe_kernel<8><<<g, t, 0, s>>>(iters, seed, out, cycles);
         break;
+    case 9: probe_kernel<9><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
+    case 10: probe_kernel<10><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
+    case 11: probe_kernel<11><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
+    case 12: probe_kernel<12><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
+    case 13: probe_kernel<13><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
     default: return static_cast<int>(hipErrorInvalidValue);
     }
     return static_cast<int>(hipGetLastError());
