@@ -1036,6 +1036,9 @@ def main(argv=None) -> int:
                     help="only the roofline kernel's ablation builds (probe/libqi_fp6_ablate_*.so), printed as JSON")
     ap.add_argument("--w4a16-block-only", action="store_true",
                     help="only the W4A16 block (config 2), printed as JSON (for kernel traces)")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="only the attention extra (4352 tokens x 24 heads) and the encoder's W4A16 linears, "
+                         "printed as JSON (for kernel traces)")
     ap.add_argument("--library-only", action="store_true",
                     help="only the calibration: the vendor library's plain fp16 / int8 GEMMs at the block's shapes")
     args = ap.parse_args(argv)
@@ -1063,6 +1066,9 @@ def main(argv=None) -> int:
         return 0
     if args.ablate_w4a4:
         print(json.dumps({"w4a4_ablation": ablate_w4a4()}), flush=True)
+        return 0
+    if args.attention_only:
+        print(json.dumps({"attention": bench_attention(), "encoder_w4a16_m300": bench_encoder()}), flush=True)
         return 0
     if args.w4a16_block_only:
         blk16 = Block(q.SCHEME_W4A16, 3)
