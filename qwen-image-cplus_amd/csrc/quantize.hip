@@ -14,6 +14,7 @@
 // shuffles.  A row of any length is just more chunks, so there is no per-row
 // LDS limit, and the grid has m * k / 256 wavefronts to spread over the CUs.
 
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -268,6 +269,113 @@ __global__ __launch_bounds__(32 / RPW * WAVE) void quantize_fp6_strip_kernel(
         out[idx] = reinterpret_cast<const uint4 *>(blocks)[idx];
 }
 
+// The strip quantiser as a persistent, software-pipelined kernel (rows >=
+// 2048): the grid's workgroups walk the (32-row tile, chunk) items with
+// stride gridDim.x, and the next item's inputs are loaded while the current
+// item is quantised and stored, so the load latency hides behind the vector
+// work instead of adding to it.  Same arithmetic, codes and layout as
+// quantize_fp6_strip_kernel.  The LDS hand-offs use a bare barrier after an
+// LDS-only wait: __syncthreads' release fence would also wait for the next
+// item's loads.
+template <typename In, int RPW, typename Producer = NoProducer>
+__global__ __launch_bounds__(32 / RPW * WAVE) void quantize_fp6_stream_kernel(
+    const In *__restrict__ x, uint8_t *__restrict__ codes, uint16_t *__restrict__ scales, int m, int k, int items,
+    Producer produce = Producer{}) {
+    using Vals = typename std::conditional<Producer::active, float, In>::type;
+    constexpr int NWV = 32 / RPW;
+    __shared__ float lds[NWV][256];
+    __shared__ __attribute__((aligned(16))) uint32_t blocks[4 * FP6_BLOCK / 4];
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int wave = threadIdx.x >> 6;
+    const int groups = k >> 6, chunks = k >> 8;
+    float *buf = lds[wave];
+    const int sl = (lane & 15) >> 2, p = lane & 3, gb = lane >> 4;
+
+    // Raw input words, converted where they are used: loads are
+    // unconditional (rows past m read row m - 1 and are zeroed later), so
+    // the compiler waits for them only at their first use.
+    using Raw = typename std::conditional<__is_same(In, uint16_t), uint2, float4>::type;
+    auto load = [&](int item, Raw (&dst)[RPW]) {
+        const int tile = item / chunks, c = item - tile * chunks;
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            const int row = min(tile * 32 + wave * RPW + i, m - 1);
+            dst[i] = *reinterpret_cast<const Raw *>(x + static_cast<size_t>(row) * k + c * 256 + lane * 4);
+        }
+    };
+    auto widen = [&](const Raw &r, float (&v)[4]) {
+        if constexpr (__is_same(In, uint16_t)) {
+            v[0] = h2f(static_cast<uint16_t>(r.x & 0xFFFFu));
+            v[1] = h2f(static_cast<uint16_t>(r.x >> 16));
+            v[2] = h2f(static_cast<uint16_t>(r.y & 0xFFFFu));
+            v[3] = h2f(static_cast<uint16_t>(r.y >> 16));
+        } else {
+            v[0] = r.x;
+            v[1] = r.y;
+            v[2] = r.z;
+            v[3] = r.w;
+        }
+    };
+    // One item: quantise `cur` (item `item`) after issuing the loads of item
+    // `next` into `nxt`.  Two named buffers alternate (the loop below is
+    // unrolled by two), so no register copy waits for the next loads.
+    auto step = [&](int item, Raw (&cur)[RPW], Raw (&nxt)[RPW]) {
+        // Unconditional (the last items reload item items - 1, unused), so
+        // that the waits for `cur` do not also wait for these loads.
+        load(min(item + static_cast<int>(gridDim.x), items - 1), nxt);
+        const int tile = item / chunks, c = item - tile * chunks;
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            const int row = tile * 32 + wave * RPW + i;
+            float v[4];
+            widen(cur[i], v);
+            if (row < m) {
+                produce(row, c * 256 + lane * 4, v);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j] = 0.f;
+            }
+            int q[4];
+            uint16_t scale_bits;
+            quantize_chunk<Vals>(v, buf, lane, q, scale_bits);
+            const int r32 = wave * RPW + i;
+            const uint32_t bits =
+                e2m3_of(q[0]) | (e2m3_of(q[1]) << 6) | (e2m3_of(q[2]) << 12) | (e2m3_of(q[3]) << 18);
+            const uint32_t nb = dpp_u32<0x101>(bits);  // row_shl:1 -- lane + 1 (unused by p = 3)
+            const int slot = (sl >> 1) * 32 + r32;
+            uint32_t *dst = blocks + (gb * FP6_BLOCK + ((sl & 1) ? FP6_HALF0 + slot * 12 : slot * 16)) / 4;
+            if (p < 3)
+                dst[p] = (bits >> (8 * p)) | (nb << (24 - 8 * p));
+            else if ((sl & 1) == 0)
+                dst[3] = scale_bits;
+            if (scales && (lane & 15) == 0)
+                scales[(static_cast<size_t>(tile) * groups + c * 4 + gb) * 32 + r32] = scale_bits;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        uint4 *out = reinterpret_cast<uint4 *>(codes + (static_cast<size_t>(tile) * groups + c * 4) * FP6_BLOCK);
+        for (int idx = threadIdx.x; idx < 4 * FP6_BLOCK / 16; idx += NWV * WAVE)
+            out[idx] = reinterpret_cast<const uint4 *>(blocks)[idx];
+        // The block reads above complete before any wave rewrites blocks.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+    int item = blockIdx.x;
+    if (item >= items) return;  // whole workgroup
+    Raw ra[RPW], rb[RPW];
+    load(item, ra);
+    for (;;) {
+        step(item, ra, rb);
+        item += gridDim.x;
+        if (item >= items) break;
+        step(item, rb, ra);
+        item += gridDim.x;
+        if (item >= items) break;
+    }
+}
+
 __global__ void f32_to_f16_kernel(const float *__restrict__ src, uint16_t *__restrict__ out,
                                   unsigned long long count) {
     const unsigned long long stride = static_cast<unsigned long long>(gridDim.x) * blockDim.x * 4;
@@ -295,7 +403,16 @@ static int launch_fp6_strip(const In *x, void *codes, void *scales, int m, int k
     const int chunks = k / 256;
     if (chunks > 65535) return kInvalid;
     const dim3 grid(static_cast<unsigned>((m + 31) / 32), static_cast<unsigned>(chunks));
-    if (m >= 1024)
+    if (m >= 2048) {
+        // Persistent and pipelined (measured 3-4 % faster from 4352 rows;
+        // slower at 1024).
+        const long long items = static_cast<long long>((m + 31) / 32) * chunks;
+        if (items > 0x7FFFFFFFLL) return kInvalid;
+        const long long wgs = std::min<long long>(items, 4LL * device_cus());
+        quantize_fp6_stream_kernel<In, 4, Producer><<<dim3(static_cast<unsigned>(wgs)), dim3(8 * WAVE), 0, stream>>>(
+            x, static_cast<uint8_t *>(codes), static_cast<uint16_t *>(scales), m, k, static_cast<int>(items),
+            produce);
+    } else if (m >= 1024)
         quantize_fp6_strip_kernel<In, 4, Producer><<<grid, dim3(8 * WAVE), 0, stream>>>(
             x, static_cast<uint8_t *>(codes), static_cast<uint16_t *>(scales), m, k, produce);
     else

@@ -95,7 +95,8 @@ def tiled_scales(scales: np.ndarray, rows: int) -> np.ndarray:
     return scales.reshape(rows // 32, 32, G).transpose(0, 2, 1).reshape(rows, G)
 
 
-@pytest.mark.parametrize("m,k,half", [(16, 256, False), (37, 768, True), (128, 3072, False), (1056, 512, True)])
+@pytest.mark.parametrize("m,k,half", [(16, 256, False), (37, 768, True), (128, 3072, False), (1056, 512, True),
+                                      (2100, 1024, True), (2083, 768, False)])
 def test_fp6_quantizer_matches_codes(dev, m, k, half):
     import qwen_image_hip.ops as ops
     x = heavy_tailed(m, k, 31 + m)

@@ -15,7 +15,7 @@ def _dev(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
 
 
-@pytest.mark.parametrize("m,k,split", [(1, 256, 0), (300, 3072, 37), (64, 12288, 64)])
+@pytest.mark.parametrize("m,k,split", [(1, 256, 0), (300, 3072, 37), (64, 12288, 64), (2100, 3072, 2048)])
 def test_layer_norm_scale_and_fused_quantiser(dev, m, k, split):
     print(f"layer norm m={m} k={k} split={split}", flush=True)
     import qwen_image_hip.ops as ops
@@ -37,7 +37,7 @@ def test_layer_norm_scale_and_fused_quantiser(dev, m, k, split):
     np.testing.assert_array_equal(fused.cpu().numpy(), plain.cpu().numpy())
 
 
-@pytest.mark.parametrize("m,k", [(5, 256), (300, 12288)])
+@pytest.mark.parametrize("m,k", [(5, 256), (300, 12288), (2050, 1024)])
 def test_swiglu_and_fused_quantiser(dev, m, k):
     print(f"swiglu m={m} k={k}", flush=True)
     import qwen_image_hip.ops as ops
