@@ -173,7 +173,8 @@ long long qi_hip_w4a16_workspace_bytes(int m, int m_split, int n, int k);
 
 /* The kernel shape the W4A16 GEMMs above choose for m rows and n_out
  * outputs per stream: 0 GEMV (m <= 16), 1 K-split 64 x 64 tiles, 3 tiled
- * 64 x 64, 4 tiled 128 x 192, 5 tiled 256 x 256, 6 tiled 128 x 128; -1 for
+ * 64 x 64, 4 tiled 128 x 192, 5 tiled 256 x 256, 6 tiled 128 x 128, 7 tiled
+ * 64 x 128; -1 for
  * m or n_out <= 0.  A query only (tests and tuning): no
  * device work.  No counterpart in the reference, whose one W4A16 kernel has
  * a fixed tile (gemm.cu:191-268). */

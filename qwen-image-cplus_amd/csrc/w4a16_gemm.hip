@@ -680,7 +680,14 @@ static int select_w4a16_tiles(int m, int n_out) {
     // 68.4, 64 x 12288 x 3072 16.9 / 20.2 / 20.3, 128 x 9216 x 3072 30.7 /
     // 24.2 / 22.0, 256 x 9216 x 3072 47.0 / 35.8 / 30.6, 256 x 12288 x 3072
     // 45.6 / 40.0 / 31.9).
-    if (m <= 256) return static_cast<long long>((m + 63) / 64) * ((n_out + 63) / 64) < 256 ? 1 : 3;
+    const long long tiles64 = static_cast<long long>((m + 63) / 64) * ((n_out + 63) / 64);
+    // Short M with very many 64 x 64 tiles (an encoder's 300 prompt rows
+    // through a 37888-wide gate + up): 64 x 128 tiles, each activation
+    // fragment read for two weight tiles (300 x 37888 x 3584: 126 -> 114 us;
+    // at 768 - 1536 tiles 64 x 64 stays faster, e.g. 256 x 9216 x 3072 30.4
+    // against 37.3).
+    if (m <= 512 && tiles64 >= 2048 && n_out % 128 == 0) return 7;
+    if (m <= 256) return tiles64 < 256 ? 1 : 3;
     // 128 x 192 tiles once they make three quarters of a round of
     // workgroups (two per CU) or more, else 64 x 64 tiles (measured:
     // 1024 x 12288 x 3072 123.5 -> 94.8 us with 512 large tiles; 1536 x 3072
@@ -725,7 +732,7 @@ static size_t splitk_bytes(int m, int n_out, int k) {
     return s > 1 ? static_cast<size_t>(s) * m * n_out * 4 : 0;
 }
 
-static const int kTileRows[] = {0, 64, 32, 64, 128, 256, 128}, kTileCols[] = {0, 64, 64, 64, 192, 256, 128};
+static const int kTileRows[] = {0, 64, 32, 64, 128, 256, 128, 64}, kTileCols[] = {0, 64, 64, 64, 192, 256, 128, 128};
 
 // One launch over both streams (m_split > 0) only when its tiles fit both
 // blocks and it takes no more rounds of workgroups than stream 0 alone
@@ -788,6 +795,8 @@ static int dispatch_w4a16(const void *x, const void *codes, const void *scales, 
         return launch_tiled<8, 3, 4>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, m_split, s);
     case 5:
         return launch_tiled<16, 2, 8>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, m_split, s);
+    case 7:
+        return launch_tiled<4, 2, 4>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, m_split, s);
     default:
         return launch_tiled<8, 2, 4>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, m_split, s);
     }

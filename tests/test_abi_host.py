@@ -115,6 +115,7 @@ def test_error_wording_mirrors_reference():
     (4096, 9216, 4), (4096, 3072, 4), (1152, 18432, 4), (600, 18432, 4),
     (4096, 12288, 5), (12288, 12288, 5),
     (1152, 1024, 6),
+    (300, 37888, 7), (256, 37888, 7), (512, 32768, 7), (600, 37888, 3),  # 64 x 128: short M, >= 2048 small tiles
 ])
 def test_w4a16_tile_choice(m, n_out, cfg):
     assert qwen_image_hip.load().qi_hip_w4a16_tiles(m, n_out) == cfg

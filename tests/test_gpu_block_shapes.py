@@ -92,6 +92,7 @@ W4A16_CASES = [
     (256, 3072, 12288, 1),    # text MLP down: K-split
     (1152, 1024, 256, 6),     # 128 x 128 tiles
     (1152, 18432, 128, 4),    # 128 x 192 tiles, two groups
+    (300, 32768, 512, 7),     # 64 x 128 tiles (an encoder's gate + up shape), ragged rows
 ]
 
 
