@@ -170,3 +170,44 @@ def test_noalloc_entry_point_rejects_sizes_beyond_its_array():
     assert L.qi_hip_layer_norm_scale_quantize_fp6_noalloc(16, 16, 256, 0, 16, 65537, 256, None) == INVALID
     assert L.qi_hip_layer_norm_scale_quantize_fp6_noalloc(16, 16, 256, 0, 16, 4, 300, None) == INVALID  # k % 256
     assert L.qi_hip_layer_norm_scale_quantize_fp6_noalloc(16, 16, 256, 0, 16, 0, 256, None) == 0          # no rows
+
+
+CPLUS = Path(__file__).resolve().parents[1] / "include" / "cplus" / "src" / "hip.cplus"
+
+
+def _c_to_cplus(c: str) -> str:
+    c = " ".join(c.replace("const ", "").split())
+    ptr, base = c.count("*"), c.replace("*", "").strip()
+    return "*" * ptr + {"void": "u8", "float": "f32", "int": "i32", "char": "u8", "uint32_t": "u32",
+                        "uint64_t": "u64", "long long": "i64", "unsigned long long": "u64", "qi_pack": "u8",
+                        "qi_pack_record": "u8"}[base]
+
+
+def test_cplus_binding_matches_the_header():
+    """include/cplus/src/hip.cplus (the C+ declarations a reference-side
+    package binds) declares every function of the header, with the same
+    parameter names, order and C+ types, and the reference's own four
+    declarations (cuda.cplus:45-46,53-58) unchanged."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    header = {}
+    for m in re.finditer(r"^\s*((?:const\s+)?(?:int|void|uint64_t|long long|unsigned long long)\s*\**)\s*(qi_\w+)"
+                         r"\s*\(([^)]*)\)\s*;", text, flags=re.M | re.S):
+        args = " ".join(m.group(3).split())
+        params = [] if args == "void" else [
+            (re.match(r"(.*?)(\w+)$", a.strip()).group(2), _c_to_cplus(re.match(r"(.*?)(\w+)$", a.strip()).group(1)))
+            for a in args.split(",")]
+        ret = None if m.group(1).strip() == "void" else _c_to_cplus(m.group(1))
+        header[m.group(2)] = (params, ret)
+    cplus = {}
+    for m in re.finditer(r'#\[link_name = "(qi_\w+)"\]\nextern fn (qi_\w+)\(([^)]*)\)(?: -> (\S+))?;',
+                         CPLUS.read_text()):
+        assert m.group(1) == m.group(2)
+        params = [tuple(p.strip().split(": ")) for p in m.group(3).split(",")] if m.group(3).strip() else []
+        cplus[m.group(1)] = (params, m.group(4))
+    assert set(cplus) == set(header) == set(declared_functions())
+    for name, sig in header.items():
+        assert cplus[name] == sig, name
+    # The reference's declarations, verbatim in meaning.
+    assert cplus["qi_w4a4_gemm"][0] == [("a_codes", "*u8"), ("a_scales", "*u8"), ("w_codes", "*u8"),
+                                        ("w_scales", "*u8"), ("y", "*f32"), ("m", "i32"), ("n", "i32"), ("k", "i32")]
+    assert cplus["qi_f32_to_f16"] == ([("source", "*f32"), ("out", "*u8"), ("count", "u64")], "i32")
