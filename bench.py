@@ -800,7 +800,11 @@ PROBE_BODIES = {0: "fp6 MFMA x4 (4 chains)", 1: "fp32 FMA x64", 2: "MFMA x4 + FM
                 10: "f16 32x32x4 2-block MFMA x4 (2048 outputs each)",
                 11: "f16 32x32x8 MFMA x4 (1024 outputs each)",
                 12: "f16 16x16x4 4-block MFMA x4 (1024 outputs each)",
-                13: "f16 4x4x4 16-block MFMA x4 (256 outputs each)"}
+                13: "f16 4x4x4 16-block MFMA x4 (256 outputs each)",
+                14: "body 2 held to two waves per SIMD (<= 256 registers: AGPR results in the AGPR build)",
+                15: "body 0 held to two waves per SIMD",
+                16: "body 14 with MFMA results in AGPRs (inline asm)",
+                17: "body 15 with MFMA results in AGPRs (inline asm)"}
 
 
 def probe_overlap(iters=2000):

@@ -31,6 +31,10 @@
 //  11  four independent v_mfma_f32_32x32x8_f16 (1024 outputs each)
 //  12  four independent v_mfma_f32_16x16x4_4b_f16 (1024 outputs each)
 //  13  four independent v_mfma_f32_4x4x4_16b_f16 (256 outputs each)
+//  14  body 2 in a kernel held to two waves per SIMD (overlap_kernel)
+//  15  body 0 in the same kernel
+//  16  body 14 with the MFMA results forced into AGPRs (inline asm)
+//  17  body 15 likewise
 // and records s_memtime (shader clock) around the loop.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -270,6 +274,72 @@ __global__ __launch_bounds__(256) void probe_kernel(int iters, const int *__rest
     if (lane == 0) cycles[gid >> 6] = t1 - t0;
 }
 
+// Bodies 14 and 15: body 2 (four fp6 MFMA chains interleaved with 64
+// independent FMAs) and body 0 alone, in a kernel held to two waves per SIMD
+// (at most 256 registers per lane, so in the accumulator-register build the
+// MFMA results live in AGPRs while two waves share each SIMD).
+// fp6 MFMA accumulating into accumulator registers (AGPRs), whatever the
+// build's register form.
+typedef int v6i __attribute__((ext_vector_type(6)));
+__device__ __forceinline__ void mfma6_agpr(v8i a, v8i b, v16f &c) {
+    const int one = 127;  // E8M0 2^0
+    const v6i a6 = __builtin_shufflevector(a, a, 0, 1, 2, 3, 4, 5), b6 = __builtin_shufflevector(b, b, 0, 1, 2, 3, 4, 5);
+    asm volatile("v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %3 op_sel_hi:[0,0,0] cbsz:2 blgp:2"
+                 : "+a"(c)
+                 : "v"(a6), "v"(b6), "v"(one));
+}
+
+template <bool FMA, bool AGPR = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void overlap_kernel(
+    int iters, const int *__restrict__ seed, float *__restrict__ out, unsigned long long *__restrict__ cycles) {
+    const int lane = threadIdx.x & 63;
+    v8i a[4], b;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) a[t][i] = seed[(lane + i + 8 * t) & 63];
+        b[i] = seed[(lane + 3 * i + 1) & 63];
+    }
+    float acc[64], x[16];
+#pragma unroll
+    for (int r = 0; r < 64; ++r) acc[r] = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x[r] = static_cast<float>(seed[(lane + r) & 63] & 7) * 0.25f;
+    const float y = 1.0009765625f;
+    v16f p[4] = {};
+    __syncthreads();
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) opaque(a[t]);
+        opaque(b);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            if constexpr (AGPR)
+                mfma6_agpr(a[t], b, p[t]);
+            else
+                p[t] = mfma6_acc(a[t], b, p[t]);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (FMA) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[16 * t + r] = __builtin_fmaf(x[r], y, acc[16 * t + r]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+    float s = 0.f;
+#pragma unroll
+    for (int r = 0; r < 64; ++r) s += acc[r];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s += p[t][r];
+    const int gid = blockIdx.x * blockDim.x + threadIdx.x;
+    out[gid] = s;
+    if (lane == 0) cycles[gid >> 6] = t1 - t0;
+}
+
 // Runs body `body` on `blocks` workgroups of four waves; cycles[w] receives
 // wave w's loop time in shader clocks.  Returns a hipError_t.
 extern "C" __attribute__((visibility("default"))) int qi_probe_run(int body, int blocks, int iters, const int *seed,
@@ -295,6 +365,10 @@ extern "C" __attribute__((visibility("default"))) int qi_probe_run(int body, int
     case 11: probe_kernel<11><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
     case 12: probe_kernel<12><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
     case 13: probe_kernel<13><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
+    case 14: overlap_kernel<true><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
+    case 15: overlap_kernel<false><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
+    case 16: overlap_kernel<true, true><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
+    case 17: overlap_kernel<false, true><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
     default: return static_cast<int>(hipErrorInvalidValue);
     }
     return static_cast<int>(hipGetLastError());
