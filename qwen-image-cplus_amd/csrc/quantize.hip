@@ -269,8 +269,8 @@ __global__ __launch_bounds__(32 / RPW * WAVE) void quantize_fp6_strip_kernel(
         out[idx] = reinterpret_cast<const uint4 *>(blocks)[idx];
 }
 
-// The strip quantiser as a persistent, software-pipelined kernel (rows >=
-// 2048): the grid's workgroups walk the (32-row tile, chunk) items with
+// The strip quantiser as a persistent, software-pipelined kernel (fp16
+// inputs, no producer, rows >= 2048): the grid's workgroups walk the (32-row tile, chunk) items with
 // stride gridDim.x, and the next item's inputs are loaded while the current
 // item is quantised and stored, so the load latency hides behind the vector
 // work instead of adding to it.  Same arithmetic, codes and layout as
@@ -403,9 +403,11 @@ static int launch_fp6_strip(const In *x, void *codes, void *scales, int m, int k
     const int chunks = k / 256;
     if (chunks > 65535) return kInvalid;
     const dim3 grid(static_cast<unsigned>((m + 31) / 32), static_cast<unsigned>(chunks));
-    if (m >= 2048) {
-        // Persistent and pipelined (measured 3-4 % faster from 4352 rows;
-        // slower at 1024).
+    if (m >= 2048 && !Producer::active && __is_same(In, uint16_t)) {
+        // Persistent and pipelined, for fp16 inputs without a producer
+        // (measured 3-4 % faster from 4352 rows, slower at 1024; with a
+        // producer, whose own loads are not pipelined, slower: LayerNorm
+        // 4096 x 3072 18.8 -> 22.4 us, SwiGLU 4096 x 12288 110 -> 116).
         const long long items = static_cast<long long>((m + 31) / 32) * chunks;
         if (items > 0x7FFFFFFFLL) return kInvalid;
         const long long wgs = std::min<long long>(items, 4LL * device_cus());
