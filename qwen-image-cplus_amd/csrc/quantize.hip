@@ -13,8 +13,10 @@
 // Lanes 16g..16g+15 then hold group g and reduce its absmax with 16-lane
 // shuffles.  A row of any length is just more chunks, so there is no per-row
 // LDS limit, and the grid has m * k / 256 wavefronts to spread over the CUs.
+// That form serves the QIPACK layout; the fp6 layout (the fast path) uses
+// sixteen inputs per lane (quantize_fp6_lane16_kernel), which leaves two of
+// the four stages in registers and one LDS round trip for the other two.
 
-#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -35,10 +37,14 @@ template <bool HALF>
 __device__ __forceinline__ void butterfly4(float &a, float &b, float &c, float &d) {
     const float x0 = a, x1 = b, x2 = c, x3 = d;
     const float f = HALF ? 0.5f : 1.0f;
-    a = (x0 + x1 + x2 - x3) * f;
-    b = (x0 + x1 - x2 + x3) * f;
-    c = (x0 - x1 + x2 + x3) * f;
-    d = (-x0 + x1 + x2 + x3) * f;
+    // The shared first sums: -x0 + x1 rounds to exactly -(x0 - x1), and
+    // (-(x0 - x1)) + x2 is x2 - (x0 - x1), so each output keeps the
+    // reference's three roundings in its order.
+    const float sum = x0 + x1, dif = x0 - x1;
+    a = ((sum + x2) - x3) * f;
+    b = ((sum - x2) + x3) * f;
+    c = ((dif + x2) + x3) * f;
+    d = ((x2 - dif) + x3) * f;
 }
 
 template <typename In>
@@ -64,22 +70,12 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
-}
 
 // LDS word of element i of a chunk: an XOR swizzle that makes every access
 // pattern below (4 consecutive words per lane, and the strided butterfly
 // quadruples of strides 4, 16, 64) conflict-free for 32 lanes at a time.
 __device__ __forceinline__ int swz(int i) { return i ^ ((i >> 2) & 31); }
 
-// E2M3 code of the int4 value q: |q| 0..7 -> 0, 8, 16, 20, 24, 26, 28, 30,
-// i.e. twice the nibble |q| of 0xFEDCA840, plus the sign bit 32.
-__device__ __forceinline__ uint32_t e2m3_of(int q) {
-    const uint32_t a = static_cast<uint32_t>(q < 0 ? -q : q);
-    return (__builtin_amdgcn_ubfe(0xFEDCA840u, 4 * a, 4) << 1) | (q < 0 ? 32u : 0u);
-}
 
 // One 256-element chunk held by a wave, lane l owning elements 4l .. 4l+3
 // (v, in place): the H256 rotation in the reference's exact fp32 operation
@@ -202,178 +198,167 @@ __global__ __launch_bounds__(QUANT_WAVES * WAVE) void quantize_chunks_kernel(
 // of one chunk -- the tile's blocks for the chunk's four groups, 7168
 // contiguous bytes -- assembling them in LDS and writing them with 16-byte
 // stores (one row per workgroup would scatter 4-byte stores of 32
-// workgroups over every block).  Wave w takes rows w * RPW .. + RPW - 1 and
-// issues all their loads first.  Rows past m quantise zeros; their codes are
-// written but never used.
+// workgroups over every block).  Rows past m quantise zeros; their codes
+// are written but never used.
 // No producer: the quantiser reads its input as is.
 struct NoProducer {
     static constexpr bool active = false;
     __device__ void operator()(int, int, float (&)[4]) const {}
 };
 
-template <typename In, int RPW, typename Producer = NoProducer>
-__global__ __launch_bounds__(32 / RPW * WAVE) void quantize_fp6_strip_kernel(
+// The fp6 quantiser, sixteen inputs per lane: lane (r, s) of the
+// 512-lane workgroup holds inputs 16s .. 16s + 15 of row r of the 32-row
+// tile's chunk (r = 4 * wave + lane / 16, s = lane % 16).  The H256 stages
+// of strides 1 and 4 run in registers; for strides 16 and 64 the values go
+// through a wave-private LDS row and each lane takes the 16 elements
+// s + 16x + 64y, whose two stages again run in registers, and back (16-byte
+// accesses on the home side).  A 64-group is then one quad of lanes: the
+// absmax is in-lane plus two DPP steps, and the lane's 16 codes are one
+// half-slot of the fp6 layout, converted by v_cvt_scalef32_2xpk16_fp6_f32
+// from the exact integers q (scale 1; a zero's sign is cleared).  Same
+// arithmetic, operation order and codes as quantize_chunk.
+typedef float v16f_q __attribute__((ext_vector_type(16)));
+
+typedef unsigned v6u_q __attribute__((ext_vector_type(6)));
+
+template <typename In, typename Producer = NoProducer>
+__global__ __launch_bounds__(8 * WAVE) void quantize_fp6_lane16_kernel(
     const In *__restrict__ x, uint8_t *__restrict__ codes, uint16_t *__restrict__ scales, int m, int k,
     Producer produce = Producer{}) {
-    // With a producer the values are arbitrary fp32, whatever the input type.
     using Vals = typename std::conditional<Producer::active, float, In>::type;
-    constexpr int NWV = 32 / RPW;
-    __shared__ float lds[NWV][256];
+    constexpr bool HALF = !__is_same(Vals, uint16_t);  // see butterfly4
+    constexpr float unit = HALF ? 1.0f : 16.0f;
+    constexpr int ROW = 256 + 16;  // floats per LDS row: 16 bytes of padding after every 64 values
+    // The tile's rows, then (once every wave has its values back) the
+    // tile's code blocks in the same bytes: 34 KiB, four workgroups per CU.
+    __shared__ __attribute__((aligned(16))) float rows[32 * ROW];
     __shared__ __attribute__((aligned(16))) uint32_t blocks[4 * FP6_BLOCK / 4];
-    const int lane = threadIdx.x & (WAVE - 1);
-    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
+    const int r = wave * 4 + (lane >> 4), s = lane & 15, j = s & 3;
     const int groups = k >> 6;
     const int tile = blockIdx.x, c = blockIdx.y;
-    float *buf = lds[wave];
+    const int row = tile * 32 + r;
+    auto addr = [](int e) { return e + 4 * (e >> 6); };  // padded LDS word of element e of a row
+    float *lrow = rows + r * ROW;
 
-    float in[RPW][4];
+    float v[16];
+    {
+        const int rr = min(row, m - 1);
+        const In *src = x + static_cast<size_t>(rr) * k + c * 256 + 16 * s;
+        if constexpr (__is_same(In, uint16_t) && !Producer::active) {
+            // Rows past m quantise zeros: the raw words are cleared.
+            uint4 h[2];
 #pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-        const int row = tile * 32 + wave * RPW + i;
-        if (row < m) {
-            load4<In>(x + static_cast<size_t>(row) * k + c * 256 + lane * 4, in[i]);
-            produce(row, c * 256 + lane * 4, in[i]);
+            for (int t = 0; t < 2; ++t) {
+                h[t] = *reinterpret_cast<const uint4 *>(src + 8 * t);
+                if (row >= m) h[t] = uint4{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const uint32_t w4[4] = {h[t].x, h[t].y, h[t].z, h[t].w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    v[8 * t + 2 * u] = h2f(static_cast<uint16_t>(w4[u] & 0xFFFFu));
+                    v[8 * t + 2 * u + 1] = h2f(static_cast<uint16_t>(w4[u] >> 16));
+                }
+            }
         } else {
+            // All loads first, the producer's included (it runs on the
+            // clamped row, branch-free), so that none waits for another
+            // chunk's arithmetic; rows past m are zeroed after.
+            float w[4][4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) in[i][j] = 0.f;
+            for (int t = 0; t < 4; ++t) load4<In>(src + 4 * t, w[t]);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) produce(rr, c * 256 + 16 * s + 4 * t, w[t]);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v[4 * t + u] = row < m ? w[t][u] : 0.f;
         }
     }
-    // This lane's four inputs are 4p..4p+3 of slice sl of its group (inputs
-    // 16 sl .. 16 sl + 15).  Slice sl goes to half sl & 1 of the group's
-    // block, lane slot 32 (sl >> 1) + row % 32, whose 12 code bytes are the
-    // 24-bit runs of lanes p = 0..3: lane p < 3 assembles and stores dword
-    // p.  In half 0 (16-byte slots) lane p = 3 stores the scale as dword 3.
-    const int sl = (lane & 15) >> 2, p = lane & 3, gb = lane >> 4;
+    // Strides 1 and 4.
 #pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-        float v[4] = {in[i][0], in[i][1], in[i][2], in[i][3]};
-        int q[4];
-        uint16_t scale_bits;
-        quantize_chunk<Vals>(v, buf, lane, q, scale_bits);
-        const int r32 = wave * RPW + i;
-        const uint32_t bits =
-            e2m3_of(q[0]) | (e2m3_of(q[1]) << 6) | (e2m3_of(q[2]) << 12) | (e2m3_of(q[3]) << 18);
-        const uint32_t next = dpp_u32<0x101>(bits);  // row_shl:1 -- lane + 1 (unused by p = 3)
-        const int slot = (sl >> 1) * 32 + r32;
-        uint32_t *dst = blocks + (gb * FP6_BLOCK + ((sl & 1) ? FP6_HALF0 + slot * 12 : slot * 16)) / 4;
-        if (p < 3)
-            dst[p] = (bits >> (8 * p)) | (next << (24 - 8 * p));
-        else if ((sl & 1) == 0)
-            dst[3] = scale_bits;
-        if (scales && (lane & 15) == 0)
-            scales[(static_cast<size_t>(tile) * groups + c * 4 + gb) * 32 + r32] = scale_bits;
+    for (int t = 0; t < 4; ++t) butterfly4<HALF>(v[4 * t], v[4 * t + 1], v[4 * t + 2], v[4 * t + 3]);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) butterfly4<HALF>(v[t], v[t + 4], v[t + 8], v[t + 12]);
+    // Strides 16 and 64 through the wave's LDS rows (no other wave touches
+    // them): the lane takes the 16 elements s + 16x + 64y (x, y = 0..3),
+    // whose stride-16 butterflies run over x and stride-64 ones over y, then
+    // the values go back to their home lanes.
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+        *reinterpret_cast<float4 *>(lrow + addr(16 * s + 4 * t)) = float4{v[4 * t], v[4 * t + 1], v[4 * t + 2], v[4 * t + 3]};
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    {
+        float w[4][4];  // [x][y]
+#pragma unroll
+        for (int xx = 0; xx < 4; ++xx)
+#pragma unroll
+            for (int yy = 0; yy < 4; ++yy) w[xx][yy] = lrow[addr(s + 16 * xx + 64 * yy)];
+#pragma unroll
+        for (int yy = 0; yy < 4; ++yy) butterfly4<HALF>(w[0][yy], w[1][yy], w[2][yy], w[3][yy]);
+#pragma unroll
+        for (int xx = 0; xx < 4; ++xx) butterfly4<HALF>(w[xx][0], w[xx][1], w[xx][2], w[xx][3]);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int xx = 0; xx < 4; ++xx)
+#pragma unroll
+            for (int yy = 0; yy < 4; ++yy) lrow[addr(s + 16 * xx + 64 * yy)] = w[xx][yy];
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const float4 w = *reinterpret_cast<const float4 *>(lrow + addr(16 * s + 4 * t));
+        v[4 * t] = w.x;
+        v[4 * t + 1] = w.y;
+        v[4 * t + 2] = w.z;
+        v[4 * t + 3] = w.w;
+    }
+
+    // Group (quad) absmax, fp16 scale, quotients (gemm.cu:45-48), as
+    // quantize_chunk.
+    float peak = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) peak = fmaxf(peak, fabsf(v[i]));
+    peak = fmaxf(peak, dpp_f32<0xB1>(peak));  // quad_perm [1,0,3,2]
+    peak = fmaxf(peak, dpp_f32<0x4E>(peak));  // quad_perm [2,3,0,1]
+    const uint16_t scale_bits = f2h(fmaxf((peak * (1.0f / unit)) / 7.0f, 5.9604645e-08f));
+    const float dd = h2f(scale_bits) * unit;
+    const float y = 1.0f / dd;
+    v16f_q qa, qb;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float q0 = v[i] * y;
+        const float quot = __builtin_fmaf(__builtin_fmaf(-q0, dd, v[i]), y, q0);
+        // rint by the 1.5 * 2^23 shift (|quot| < 11 here): ties to even like
+        // rintf, and a quotient in [-0.5, 0) gives +0, the reference's
+        // integer code 0, where rintf would give -0 (code 32 after the
+        // conversion).
+        const float q = __builtin_amdgcn_fmed3f((quot + 12582912.0f) - 12582912.0f, -7.0f, 7.0f);
+        if (i & 1) qb[i >> 1] = q; else qa[i >> 1] = q;
+    }
+#pragma unroll
+    for (int i = 8; i < 16; ++i) qa[i] = qb[i] = 0.f;
+    const v6u_q cw = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(qa, qb, 1.0f);
+    // Half-slot of group gb = s / 4: half j & 1, slot (j >> 1) * 32 + r.
+    const int gb = s >> 2, slot = (j >> 1) * 32 + r;
+    if ((j & 1) == 0) {
+        *reinterpret_cast<uint4 *>(blocks + (gb * FP6_BLOCK + slot * 16) / 4) = uint4{cw[0], cw[1], cw[2], scale_bits};
+    } else {
+        uint32_t *dst = blocks + (gb * FP6_BLOCK + FP6_HALF0 + slot * 12) / 4;
+        dst[0] = cw[0];
+        dst[1] = cw[1];
+        dst[2] = cw[2];
+    }
+    if (scales && j == 0) scales[(static_cast<size_t>(tile) * groups + c * 4 + gb) * 32 + r] = scale_bits;
     __syncthreads();
     uint4 *out = reinterpret_cast<uint4 *>(codes + (static_cast<size_t>(tile) * groups + c * 4) * FP6_BLOCK);
-    for (int idx = threadIdx.x; idx < 4 * FP6_BLOCK / 16; idx += NWV * WAVE)
+    for (int idx = threadIdx.x; idx < 4 * FP6_BLOCK / 16; idx += 8 * WAVE)
         out[idx] = reinterpret_cast<const uint4 *>(blocks)[idx];
-}
-
-// The strip quantiser as a persistent, software-pipelined kernel (fp16
-// inputs, no producer, rows >= 2048): the grid's workgroups walk the (32-row tile, chunk) items with
-// stride gridDim.x, and the next item's inputs are loaded while the current
-// item is quantised and stored, so the load latency hides behind the vector
-// work instead of adding to it.  Same arithmetic, codes and layout as
-// quantize_fp6_strip_kernel.  The LDS hand-offs use a bare barrier after an
-// LDS-only wait: __syncthreads' release fence would also wait for the next
-// item's loads.
-template <typename In, int RPW, typename Producer = NoProducer>
-__global__ __launch_bounds__(32 / RPW * WAVE) void quantize_fp6_stream_kernel(
-    const In *__restrict__ x, uint8_t *__restrict__ codes, uint16_t *__restrict__ scales, int m, int k, int items,
-    Producer produce = Producer{}) {
-    using Vals = typename std::conditional<Producer::active, float, In>::type;
-    constexpr int NWV = 32 / RPW;
-    __shared__ float lds[NWV][256];
-    __shared__ __attribute__((aligned(16))) uint32_t blocks[4 * FP6_BLOCK / 4];
-    const int lane = threadIdx.x & (WAVE - 1);
-    const int wave = threadIdx.x >> 6;
-    const int groups = k >> 6, chunks = k >> 8;
-    float *buf = lds[wave];
-    const int sl = (lane & 15) >> 2, p = lane & 3, gb = lane >> 4;
-
-    // Raw input words, converted where they are used: loads are
-    // unconditional (rows past m read row m - 1 and are zeroed later), so
-    // the compiler waits for them only at their first use.
-    using Raw = typename std::conditional<__is_same(In, uint16_t), uint2, float4>::type;
-    auto load = [&](int item, Raw (&dst)[RPW]) {
-        const int tile = item / chunks, c = item - tile * chunks;
-#pragma unroll
-        for (int i = 0; i < RPW; ++i) {
-            const int row = min(tile * 32 + wave * RPW + i, m - 1);
-            dst[i] = *reinterpret_cast<const Raw *>(x + static_cast<size_t>(row) * k + c * 256 + lane * 4);
-        }
-    };
-    auto widen = [&](const Raw &r, float (&v)[4]) {
-        if constexpr (__is_same(In, uint16_t)) {
-            v[0] = h2f(static_cast<uint16_t>(r.x & 0xFFFFu));
-            v[1] = h2f(static_cast<uint16_t>(r.x >> 16));
-            v[2] = h2f(static_cast<uint16_t>(r.y & 0xFFFFu));
-            v[3] = h2f(static_cast<uint16_t>(r.y >> 16));
-        } else {
-            v[0] = r.x;
-            v[1] = r.y;
-            v[2] = r.z;
-            v[3] = r.w;
-        }
-    };
-    // One item: quantise `cur` (item `item`) after issuing the loads of item
-    // `next` into `nxt`.  Two named buffers alternate (the loop below is
-    // unrolled by two), so no register copy waits for the next loads.
-    auto step = [&](int item, Raw (&cur)[RPW], Raw (&nxt)[RPW]) {
-        // Unconditional (the last items reload item items - 1, unused), so
-        // that the waits for `cur` do not also wait for these loads.
-        load(min(item + static_cast<int>(gridDim.x), items - 1), nxt);
-        const int tile = item / chunks, c = item - tile * chunks;
-#pragma unroll
-        for (int i = 0; i < RPW; ++i) {
-            const int row = tile * 32 + wave * RPW + i;
-            float v[4];
-            widen(cur[i], v);
-            if (row < m) {
-                produce(row, c * 256 + lane * 4, v);
-            } else {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) v[j] = 0.f;
-            }
-            int q[4];
-            uint16_t scale_bits;
-            quantize_chunk<Vals>(v, buf, lane, q, scale_bits);
-            const int r32 = wave * RPW + i;
-            const uint32_t bits =
-                e2m3_of(q[0]) | (e2m3_of(q[1]) << 6) | (e2m3_of(q[2]) << 12) | (e2m3_of(q[3]) << 18);
-            const uint32_t nb = dpp_u32<0x101>(bits);  // row_shl:1 -- lane + 1 (unused by p = 3)
-            const int slot = (sl >> 1) * 32 + r32;
-            uint32_t *dst = blocks + (gb * FP6_BLOCK + ((sl & 1) ? FP6_HALF0 + slot * 12 : slot * 16)) / 4;
-            if (p < 3)
-                dst[p] = (bits >> (8 * p)) | (nb << (24 - 8 * p));
-            else if ((sl & 1) == 0)
-                dst[3] = scale_bits;
-            if (scales && (lane & 15) == 0)
-                scales[(static_cast<size_t>(tile) * groups + c * 4 + gb) * 32 + r32] = scale_bits;
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        uint4 *out = reinterpret_cast<uint4 *>(codes + (static_cast<size_t>(tile) * groups + c * 4) * FP6_BLOCK);
-        for (int idx = threadIdx.x; idx < 4 * FP6_BLOCK / 16; idx += NWV * WAVE)
-            out[idx] = reinterpret_cast<const uint4 *>(blocks)[idx];
-        // The block reads above complete before any wave rewrites blocks.
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-    };
-    int item = blockIdx.x;
-    if (item >= items) return;  // whole workgroup
-    Raw ra[RPW], rb[RPW];
-    load(item, ra);
-    for (;;) {
-        step(item, ra, rb);
-        item += gridDim.x;
-        if (item >= items) break;
-        step(item, rb, ra);
-        item += gridDim.x;
-        if (item >= items) break;
-    }
 }
 
 __global__ void f32_to_f16_kernel(const float *__restrict__ src, uint16_t *__restrict__ out,
@@ -403,23 +388,8 @@ static int launch_fp6_strip(const In *x, void *codes, void *scales, int m, int k
     const int chunks = k / 256;
     if (chunks > 65535) return kInvalid;
     const dim3 grid(static_cast<unsigned>((m + 31) / 32), static_cast<unsigned>(chunks));
-    if (m >= 2048 && !Producer::active && __is_same(In, uint16_t)) {
-        // Persistent and pipelined, for fp16 inputs without a producer
-        // (measured 3-4 % faster from 4352 rows, slower at 1024; with a
-        // producer, whose own loads are not pipelined, slower: LayerNorm
-        // 4096 x 3072 18.8 -> 22.4 us, SwiGLU 4096 x 12288 110 -> 116).
-        const long long items = static_cast<long long>((m + 31) / 32) * chunks;
-        if (items > 0x7FFFFFFFLL) return kInvalid;
-        const long long wgs = std::min<long long>(items, 4LL * device_cus());
-        quantize_fp6_stream_kernel<In, 4, Producer><<<dim3(static_cast<unsigned>(wgs)), dim3(8 * WAVE), 0, stream>>>(
-            x, static_cast<uint8_t *>(codes), static_cast<uint16_t *>(scales), m, k, static_cast<int>(items),
-            produce);
-    } else if (m >= 1024)
-        quantize_fp6_strip_kernel<In, 4, Producer><<<grid, dim3(8 * WAVE), 0, stream>>>(
-            x, static_cast<uint8_t *>(codes), static_cast<uint16_t *>(scales), m, k, produce);
-    else
-        quantize_fp6_strip_kernel<In, 2, Producer><<<grid, dim3(16 * WAVE), 0, stream>>>(
-            x, static_cast<uint8_t *>(codes), static_cast<uint16_t *>(scales), m, k, produce);
+    quantize_fp6_lane16_kernel<In, Producer><<<grid, dim3(8 * WAVE), 0, stream>>>(
+        x, static_cast<uint8_t *>(codes), static_cast<uint16_t *>(scales), m, k, produce);
     return launch_status();
 }
 
