@@ -804,7 +804,9 @@ PROBE_BODIES = {0: "fp6 MFMA x4 (4 chains)", 1: "fp32 FMA x64", 2: "MFMA x4 + FM
                 14: "body 2 held to two waves per SIMD (<= 256 registers: AGPR results in the AGPR build)",
                 15: "body 0 held to two waves per SIMD",
                 16: "body 14 with MFMA results in AGPRs (inline asm)",
-                17: "body 15 with MFMA results in AGPRs (inline asm)"}
+                17: "body 15 with MFMA results in AGPRs (inline asm)",
+                18: "f16 32x32x16 MFMA x4 (the attention's)",
+                19: "f16 16x16x32 MFMA x4 (the W4A16 GEMM's)"}
 
 
 def probe_overlap(iters=2000):

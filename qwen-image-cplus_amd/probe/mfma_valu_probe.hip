@@ -35,6 +35,8 @@
 //  15  body 0 in the same kernel
 //  16  body 14 with the MFMA results forced into AGPRs (inline asm)
 //  17  body 15 likewise
+//  18  four independent v_mfma_f32_32x32x16_f16 (the attention's)
+//  19  four independent v_mfma_f32_16x16x32_f16 (the W4A16 GEMM's)
 // and records s_memtime (shader clock) around the loop.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -208,6 +210,19 @@ __global__ __launch_bounds__(256) void probe_kernel(int iters, const int *__rest
                 v4i v = lds[(r + it) & 7][64 * wv + lane];
                 rd[r] += v;
             }
+        } else if constexpr (BODY == 18 || BODY == 19) {
+            // The fp16 MFMAs of the product kernels: 32x32x16 (attention)
+            // and 16x16x32 (W4A16), four chains.
+            typedef _Float16 v8h_p __attribute__((ext_vector_type(8)));
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const v8h_p ha8 = __builtin_bit_cast(v8h_p, __builtin_shufflevector(a[t], a[t], 0, 1, 2, 3));
+                const v8h_p hb8 = __builtin_bit_cast(v8h_p, __builtin_shufflevector(b, b, 0, 1, 2, 3));
+                if constexpr (BODY == 18)
+                    p[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ha8, hb8, p[t], 0, 0, 0);
+                else
+                    w4[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ha8, hb8, w4[t], 0, 0, 0);
+            }
         } else if constexpr (BODY >= 9 && BODY <= 13) {
             // Output-rate of the small-K MFMA shapes (four accumulation
             // chains; operands made opaque above through a and b).
@@ -258,7 +273,7 @@ __global__ __launch_bounds__(256) void probe_kernel(int iters, const int *__rest
     }
 #pragma unroll
     for (int r = 0; r < 8; ++r) s += static_cast<float>(rd[r][0] + rd[r][1] + rd[r][2] + rd[r][3]);
-    if constexpr (BODY >= 9) {
+    if constexpr (BODY >= 9 && BODY <= 19) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
 #pragma unroll
@@ -368,6 +383,8 @@ extern "C" __attribute__((visibility("default"))) int qi_probe_run(int body, int
     case 14: overlap_kernel<true><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
     case 15: overlap_kernel<false><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
     case 16: overlap_kernel<true, true><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
+    case 18: probe_kernel<18><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
+    case 19: probe_kernel<19><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
     case 17: overlap_kernel<false, true><<<g, t, 0, s>>>(iters, seed, out, cycles); break;
     default: return static_cast<int>(hipErrorInvalidValue);
     }
