@@ -217,6 +217,7 @@ class StepW4A16:
         from qwen_image_hip import ops
 
         self.ops = ops
+        self.side = None if one_stream else torch.cuda.Stream()
         g = torch.Generator(device="cuda")
         g.manual_seed(seed)
         self.block = block
@@ -227,8 +228,39 @@ class StepW4A16:
             "qkv": torch.empty((3, m, HIDDEN), dtype=torch.float16, device="cuda"),
             "h": torch.empty((m, MLP), dtype=torch.float16, device="cuda"),
         }
+        # Two streams: each stream's rows of the same buffers, its own records.
+        rows, r0 = {}, 0
+        for stream, ms in STREAMS.items():
+            rows[stream] = (r0, r0 + ms)
+            r0 += ms
+        self.rows = rows
+        self.qkv_s = {stream: torch.empty((3, ms, HIDDEN), dtype=torch.float16, device="cuda")
+                      for stream, ms in STREAMS.items()}
+
+    def _two_streams(self):
+        ops, b, f16 = self.ops, self.b, self.ops.torch.float16
+
+        def run_phase(stream, phase):
+            r0, r1 = self.rows[stream]
+            L = lambda name: self.block.layers[(stream, name)]  # noqa: E731
+            x, y, h = b["x"][r0:r1], b["y"][r0:r1], b["h"][r0:r1]
+            if phase == "qkv":
+                r = L("qkv")
+                ops.w4a16_gemm(x, r.tiled_codes, r.tiled_scales, out_dtype=f16, y=self.qkv_s[stream], n_part=HIDDEN)
+            elif phase == "out":
+                r = L("to_out")
+                ops.w4a16_gemm(x, r.tiled_codes, r.tiled_scales, out_dtype=f16, y=y)
+            else:
+                r = L("mlp_up")
+                ops.w4a16_gemm(x, r.tiled_codes, r.tiled_scales, out_dtype=f16, gelu=True, y=h)
+                r = L("mlp_down")
+                ops.w4a16_gemm(h, r.tiled_codes, r.tiled_scales, out_dtype=f16, y=y)
+
+        two_streams(run_phase, self.side)
 
     def __call__(self):
+        if self.side is not None:
+            return self._two_streams()
         ops, b, f16 = self.ops, self.b, self.ops.torch.float16
         L = lambda name: self.block.layers[("dual", name)]  # noqa: E731
         split = STREAMS["image"]
@@ -1078,11 +1110,16 @@ def main(argv=None) -> int:
         return 0
     if args.w4a16_block_only:
         blk16 = Block(q.SCHEME_W4A16, 3)
-        step16 = StepW4A16(blk16, 4)
-        ms16 = time_fn(step16, args.steps, args.warmup)
-        tf16 = block_ops() / (ms16 * 1e-3) / 1e12
-        print(json.dumps({"w4a16_block": {"ms_per_step": round(ms16, 4), "TFLOP_s": round(tf16, 1),
-                                          "frac_fp16_peak": round(tf16 * 1e12 / PEAK_FP16_FLOPS, 4)}}), flush=True)
+        out = {}
+        for name, one in (("one_stream", True), ("two_streams", False)):
+            step16 = StepW4A16(blk16, 4, one_stream=one)
+            ms16 = time_fn(step16, args.steps, args.warmup)
+            tf16 = block_ops() / (ms16 * 1e-3) / 1e12
+            out[name] = {"ms_per_step": round(ms16, 4), "TFLOP_s": round(tf16, 1),
+                         "frac_fp16_peak": round(tf16 * 1e12 / PEAK_FP16_FLOPS, 4)}
+            torch.cuda.synchronize()
+            out[name]["y_checksum"] = float(step16.b["y"].float().abs().sum())
+        print(json.dumps({"w4a16_block": out}), flush=True)
         return 0
     if args.probe_overlap:
         print(json.dumps({"mfma_valu_probe": probe_overlap()}), flush=True)
