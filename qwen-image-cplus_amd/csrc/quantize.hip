@@ -14,7 +14,7 @@
 // shuffles.  A row of any length is just more chunks, so there is no per-row
 // LDS limit, and the grid has m * k / 256 wavefronts to spread over the CUs.
 // That form serves the QIPACK layout; the fp6 layout (the fast path) uses
-// sixteen inputs per lane (quantize_fp6_lane16_kernel), which leaves two of
+// sixteen inputs per lane (quantize_lane16_kernel), which leaves two of
 // the four stages in registers and one LDS round trip for the other two.
 
 #include <mutex>
@@ -221,8 +221,11 @@ typedef float v16f_q __attribute__((ext_vector_type(16)));
 
 typedef unsigned v6u_q __attribute__((ext_vector_type(6)));
 
-template <typename In, typename Producer = NoProducer>
-__global__ __launch_bounds__(8 * WAVE) void quantize_fp6_lane16_kernel(
+// FMT 1 writes the fp6 layout (the code blocks assembled in LDS, 16-byte
+// stores); FMT 0 the QIPACK layout (each lane's 16 nibbles as one 8-byte
+// store, scales [m, k/64]).
+template <typename In, typename Producer = NoProducer, int FMT = 1>
+__global__ __launch_bounds__(8 * WAVE) void quantize_lane16_kernel(
     const In *__restrict__ x, uint8_t *__restrict__ codes, uint16_t *__restrict__ scales, int m, int k,
     Producer produce = Producer{}) {
     using Vals = typename std::conditional<Producer::active, float, In>::type;
@@ -329,23 +332,45 @@ __global__ __launch_bounds__(8 * WAVE) void quantize_fp6_lane16_kernel(
     const uint16_t scale_bits = f2h(fmaxf((peak * (1.0f / unit)) / 7.0f, 5.9604645e-08f));
     const float dd = h2f(scale_bits) * unit;
     const float y = 1.0f / dd;
-    v16f_q qa, qb;
+    // rint by the shift M = 1.5 * 2^23 (|quot| < 11 here): quot + M rounds to
+    // M + rint(quot), ties to even like rintf, and is clamped there; its low
+    // mantissa bits are the two's-complement code (the QIPACK nibble), and
+    // subtracting M gives the integer as a float, +0 for a quotient in
+    // [-0.5, 0) (the reference's integer code 0, where rintf would give -0,
+    // code 32 after the fp6 conversion).
+    constexpr float M = 12582912.0f;
+    float qs[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const float q0 = v[i] * y;
         const float quot = __builtin_fmaf(__builtin_fmaf(-q0, dd, v[i]), y, q0);
-        // rint by the 1.5 * 2^23 shift (|quot| < 11 here): ties to even like
-        // rintf, and a quotient in [-0.5, 0) gives +0, the reference's
-        // integer code 0, where rintf would give -0 (code 32 after the
-        // conversion).
-        const float q = __builtin_amdgcn_fmed3f((quot + 12582912.0f) - 12582912.0f, -7.0f, 7.0f);
+        qs[i] = __builtin_amdgcn_fmed3f(quot + M, M - 7.0f, M + 7.0f);
+    }
+    const int gb = s >> 2;
+    if constexpr (FMT == 0) {
+        uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            w0 |= (__builtin_bit_cast(uint32_t, qs[i]) & 15u) << (4 * i);
+            w1 |= (__builtin_bit_cast(uint32_t, qs[8 + i]) & 15u) << (4 * i);
+        }
+        if (row < m) {
+            *reinterpret_cast<uint2 *>(codes + static_cast<size_t>(row) * (k >> 1) + c * 128 + s * 8) = uint2{w0, w1};
+            if (j == 0) scales[static_cast<size_t>(row) * groups + c * 4 + gb] = scale_bits;
+        }
+        return;
+    }
+    v16f_q qa, qb;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float q = qs[i] - M;
         if (i & 1) qb[i >> 1] = q; else qa[i >> 1] = q;
     }
 #pragma unroll
     for (int i = 8; i < 16; ++i) qa[i] = qb[i] = 0.f;
     const v6u_q cw = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(qa, qb, 1.0f);
     // Half-slot of group gb = s / 4: half j & 1, slot (j >> 1) * 32 + r.
-    const int gb = s >> 2, slot = (j >> 1) * 32 + r;
+    const int slot = (j >> 1) * 32 + r;
     if ((j & 1) == 0) {
         *reinterpret_cast<uint4 *>(blocks + (gb * FP6_BLOCK + slot * 16) / 4) = uint4{cw[0], cw[1], cw[2], scale_bits};
     } else {
@@ -388,7 +413,7 @@ static int launch_fp6_strip(const In *x, void *codes, void *scales, int m, int k
     const int chunks = k / 256;
     if (chunks > 65535) return kInvalid;
     const dim3 grid(static_cast<unsigned>((m + 31) / 32), static_cast<unsigned>(chunks));
-    quantize_fp6_lane16_kernel<In, Producer><<<grid, dim3(8 * WAVE), 0, stream>>>(
+    quantize_lane16_kernel<In, Producer><<<grid, dim3(8 * WAVE), 0, stream>>>(
         x, static_cast<uint8_t *>(codes), static_cast<uint16_t *>(scales), m, k, produce);
     return launch_status();
 }
@@ -407,6 +432,13 @@ static int launch_quantize(const In *x, void *codes, void *scales, int m, int k,
         return kInvalid;
     const int chunks = k / 256;
     if (FMT == 1) return launch_fp6_strip<In>(x, codes, scales, m, k, stream, NoProducer{});
+    if (reinterpret_cast<uintptr_t>(codes) % 8 == 0 && chunks <= 65535) {
+        // Sixteen inputs per lane, 8-byte code stores (see the kernel).
+        const dim3 grid(static_cast<unsigned>((m + 31) / 32), static_cast<unsigned>(chunks));
+        quantize_lane16_kernel<In, NoProducer, 0><<<grid, dim3(8 * WAVE), 0, stream>>>(
+            x, static_cast<uint8_t *>(codes), static_cast<uint16_t *>(scales), m, k, NoProducer{});
+        return launch_status();
+    }
     // Several chunks per wave when there are rows enough to fill the chip.
     if (m >= 1024) {
         constexpr int CPW = 4;
