@@ -11,8 +11,8 @@
 // loads (one 8-byte code load and one scale pair per lane each) in flight.
 // The activations are staged in LDS, and the wavefronts' partial sums are
 // added through LDS.  Three kernels:
-//   * w4a16_gemv_dot2_kernel (m = 1, 2): vector unit, dot2 on the fp16
-//     integers 1024 + c with the factored per-group scale step, two weight
+//   * w4a16_gemv_dot2_kernel (m = 1, 2): vector unit, dot2 on the codes
+//     as exact fp16 integers with the factored per-group scale step, two weight
 //     rows per lane and a wave-local x slice (its own layout, described at
 //     the kernel);
 //   * w4a16_gemv_factored_kernel (m <= 16, x fits in LDS): the same
@@ -134,12 +134,12 @@ __global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_kernel(
 }
 
 // Factored form, used when x fits in LDS.  Per group g and output n:
-//   y += s (P - 1024 X) + min X,  P = sum_k x_k (1024 + c_k),  X = sum_k x_k
-// The codes enter the matrix core as the exact fp16 integers 1024 + c (a
-// bit-field insert into 0x6400, no multiply), P is exact per product and
-// summed in fp32.  -1024 X comes from the matrix core too: two MFMAs with a
-// constant -1024 weight operand start the group's accumulator, which the
-// code MFMAs then add P onto, so no separate pass over x is needed.
+//   y += s P + min X,  P = sum_k x_k c_k,  X = sum_k x_k
+// The codes become exact fp16 integers without a multiply: a bit-field
+// insert into 0x6400 gives 1024 + c and a packed fp16 add of -1024 gives c
+// (both exact), so P is exact per product and summed in fp32 with no
+// cancelled 1024 X term.  X comes from the matrix core too: two MFMAs with an
+// all-ones weight operand, so no separate pass over x is needed.
 // This is the group's dot product with the weights c s + min kept in fp32,
 // instead of first rounding every weight to fp16 as the reference's
 // dequantiser does (gemm.cu:229-230): the outputs differ from that form by
@@ -206,27 +206,31 @@ __global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_factored_kernel(
         // Bit-field insert of each nibble pair into 0x6400 (written in C, not
         // inline asm: these values feed the matrix core directly, and only
         // compiler-visible instructions get the VALU-to-MFMA wait states).
+        // A packed fp16 add of -1024 then makes them the codes c exactly.
+        const v2h m1024 = {static_cast<_Float16>(-1024.0f), static_cast<_Float16>(-1024.0f)};
         uint32_t a[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            a[i] = ((cc.x >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu);
-            a[4 + i] = ((cc.y >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu);
+            a[i] = __builtin_bit_cast(
+                uint32_t, __builtin_bit_cast(v2h, ((cc.x >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu)) + m1024);
+            a[4 + i] = __builtin_bit_cast(
+                uint32_t, __builtin_bit_cast(v2h, ((cc.y >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu)) + m1024);
         }
         const uint4 x0 = *reinterpret_cast<const uint4 *>(xrow + g * 64);
         const uint4 x1 = *reinterpret_cast<const uint4 *>(xrow + g * 64 + 32);
         // The nibble slot order of the tiled codes puts element 2i in nibble
         // i and 2i+1 in nibble 4+i, so a[i] holds elements (2i, 2i+1).
-        // p = -1024 X (every output row of the constant operand is alike),
-        // then P - 1024 X.
-        const uint4 neg1024 = {0xE400E400u, 0xE400E400u, 0xE400E400u, 0xE400E400u};
-        v4f p = {0.f, 0.f, 0.f, 0.f};
-        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, neg1024), __builtin_bit_cast(v8h, x0), p,
-                                                   0, 0, 0);
-        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, neg1024), __builtin_bit_cast(v8h, x1), p,
-                                                   0, 0, 0);
-        const float X = p[0] * (-1.0f / 1024.0f);  // exact
-        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, uint4{a[0], a[1], a[2], a[3]}),
-                                                   __builtin_bit_cast(v8h, x0), p, 0, 0, 0);
+        // X = sum x (every output row of the all-ones operand is alike),
+        // then P = sum x c.
+        const uint4 ones = {0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
+        const v4f zero = {0.f, 0.f, 0.f, 0.f};
+        v4f xs = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, ones), __builtin_bit_cast(v8h, x0),
+                                                         zero, 0, 0, 0);
+        xs = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, ones), __builtin_bit_cast(v8h, x1), xs, 0,
+                                                    0, 0);
+        const float X = xs[0];
+        v4f p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, uint4{a[0], a[1], a[2], a[3]}),
+                                                       __builtin_bit_cast(v8h, x0), zero, 0, 0, 0);
         p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, uint4{a[4], a[5], a[6], a[7]}),
                                                    __builtin_bit_cast(v8h, x1), p, 0, 0, 0);
         // Quad broadcasts (DPP quad_perm r,r,r,r) gather the four pairs.
@@ -278,15 +282,19 @@ __global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_factored_kernel(
 //   * each wave stages only its own slice of x (its groups, requested before
 //     the weights, stored once it lands), so no workgroup barrier precedes
 //     the arithmetic;
-//   * the codes enter v_dot2_f32_f16 as the fp16 integers 1024 + c (a
-//     bit-field insert into 0x6400), and the lane's share of a group is
-//     s (P - 1024 X) + min X with P = sum x (1024 + c) and X = sum x over
-//     the lane's 16 inputs (the same dot2 against ones);
+//   * the codes become the fp16 integers 1024 + c (a bit-field insert into
+//     0x6400) and then c exactly (a packed fp16 add of -1024), and the
+//     lane's share of a group is s P + min X with P = sum x c and X = sum x
+//     over the lane's 16 inputs (v_dot2_f32_f16, against ones for X);
 //   * the lanes of a row differ in lane bits 3..5: bit 3 is folded by a DPP
 //     row rotate, bits 4..5 and the waves through one LDS pass.
 // This is the group's dot product with the weights c s + min in fp32, like
-// the MFMA forms: inside the W4A16 tolerance, and bit-exact fp32(c s + min) on
-// one-hot rows.
+// the matrix-core factored form: the products are exact and only their fp32
+// sums round, so the outputs differ from the reference's (whose weights are
+// first rounded to fp16) by that weight rounding, inside the W4A16
+// tolerance, and are bit-exact fp32(c s + min) on one-hot rows.  (Using the
+// reference's fp16 weights here, exact double rounding included, measured
+// 1.35x slower on the all-blocks launch.)
 constexpr int DOT2_WAVES = 8;
 constexpr int DOT2_FB = 6;  // groups per wave and chunk: three 16-byte loads per lane
 
@@ -312,6 +320,7 @@ __global__ __launch_bounds__(DOT2_WAVES *WAVE) void w4a16_gemv_dot2_kernel(
     uint32_t magic = 0x64006400u;
     asm volatile("" : "+v"(magic));  // kept in a VGPR: lets the insert be one v_bfi_b32
     const v2h one2 = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+    const v2h m1024 = {static_cast<_Float16>(-1024.0f), static_cast<_Float16>(-1024.0f)};
     float ya[M], yb[M];
 #pragma unroll
     for (int r = 0; r < M; ++r) ya[r] = yb[r] = 0.f;
@@ -346,13 +355,17 @@ __global__ __launch_bounds__(DOT2_WAVES *WAVE) void w4a16_gemv_dot2_kernel(
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int u = 0; u < NI; ++u) {
+            // (1024 + c) - 1024 = c exactly in fp16 (one packed fp16 add per
+            // two codes), so no 1024 X term is cancelled in fp32 later.
             v2h a[8], b[8];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                a[i] = __builtin_bit_cast(v2h, ((c[u][0] >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu));
-                a[4 + i] = __builtin_bit_cast(v2h, ((c[u][1] >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu));
-                b[i] = __builtin_bit_cast(v2h, ((c[u][2] >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu));
-                b[4 + i] = __builtin_bit_cast(v2h, ((c[u][3] >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu));
+                a[i] = __builtin_bit_cast(v2h, ((c[u][0] >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu)) + m1024;
+                a[4 + i] =
+                    __builtin_bit_cast(v2h, ((c[u][1] >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu)) + m1024;
+                b[i] = __builtin_bit_cast(v2h, ((c[u][2] >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu)) + m1024;
+                b[4 + i] =
+                    __builtin_bit_cast(v2h, ((c[u][3] >> (4 * i)) & 0x000F000Fu) | (magic & ~0x000F000Fu)) + m1024;
             }
             // A group past the wave's range contributes nothing: its scale
             // and minimum are taken as zero (selected here, where the loads
@@ -374,8 +387,8 @@ __global__ __launch_bounds__(DOT2_WAVES *WAVE) void w4a16_gemv_dot2_kernel(
                     pb = __builtin_amdgcn_fdot2(b[i], xq, pb, false);
                     xl = __builtin_amdgcn_fdot2(one2, xq, xl, false);
                 }
-                ya[r] = __builtin_fmaf(ma, xl, __builtin_fmaf(sa, __builtin_fmaf(-1024.0f, xl, pa), ya[r]));
-                yb[r] = __builtin_fmaf(mb, xl, __builtin_fmaf(sb, __builtin_fmaf(-1024.0f, xl, pb), yb[r]));
+                ya[r] = __builtin_fmaf(ma, xl, __builtin_fmaf(sa, pa, ya[r]));
+                yb[r] = __builtin_fmaf(mb, xl, __builtin_fmaf(sb, pb, yb[r]));
             }
         }
     }

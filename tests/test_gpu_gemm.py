@@ -201,6 +201,21 @@ def test_w4a16_gemv(dev, m, n, k):
     got = ops.w4a16_gemv(_h(xb, dev), tc, ts).cpu().numpy()
     want = oracle.w4a16_gemm(xb, c, s, mn, precise=True)
     _close(got, want)
+    # The kernels' own arithmetic, apart from the choice of weights: the
+    # dequantising form (x too large for LDS) uses the reference's fp16
+    # weights, so against the oracle only its fp32 sums differ; the factored
+    # forms (vector unit for m <= 2, matrix core otherwise) keep c s + min in
+    # fp32, so they are checked against the float64 product with those
+    # weights (a cancelled 1024 X term would show here as about 1.5e-5).
+    if m > 2 and m * k * 2 > 48 * 1024:
+        own = rel_l2(got, want)
+    else:
+        nib = np.stack([c & 15, c >> 4], -1).reshape(n, k).astype(np.float64)
+        w = (nib * np.repeat(s.view(np.float16).astype(np.float64), 64, axis=1)
+             + np.repeat(mn.view(np.float16).astype(np.float64), 64, axis=1))
+        own = rel_l2(got, xb.view(np.float16).astype(np.float64) @ w.T)
+    print(f"  arithmetic rel-L2 {own:.3e} (bar 2e-6)", flush=True)
+    assert own <= 2e-6, own
     # The tiled GEMM entry point dispatches m <= 16 to the same kernel.
     got2 = ops.w4a16_gemm(_h(xb, dev), tc, ts).cpu().numpy()
     np.testing.assert_array_equal(got, got2)
