@@ -285,7 +285,8 @@ __global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_factored_kernel(
 //   * the codes become the fp16 integers 1024 + c (a bit-field insert into
 //     0x6400) and then c exactly (a packed fp16 add of -1024), and the
 //     lane's share of a group is s P + min X with P = sum x c and X = sum x
-//     over the lane's 16 inputs (v_dot2_f32_f16, against ones for X);
+//     over the lane's 16 inputs (v_dot2_f32_f16; X once per chunk of x as
+//     it is staged, against ones, and read back from LDS);
 //   * the lanes of a row differ in lane bits 3..5: bit 3 is folded by a DPP
 //     row rotate, bits 4..5 and the waves through one LDS pass.
 // This is the group's dot product with the weights c s + min in fp32, like
@@ -307,6 +308,7 @@ __global__ __launch_bounds__(DOT2_WAVES *WAVE) void w4a16_gemv_dot2_kernel(
     constexpr int XR = (XC + WAVE - 1) / WAVE;
     __shared__ float partial[W][4][M][16];
     __shared__ __attribute__((aligned(16))) uint16_t xs[W][M * FB * 64];
+    __shared__ float xsum[W][XC];  // [row][group][chunk pair q]: sum x over chunks q and q + 4
     const int groups = k >> 6;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
     const int h = lane >> 5, j = lane & 31, q = j >> 3, r0 = (2 * j) & 15;
@@ -316,6 +318,7 @@ __global__ __launch_bounds__(DOT2_WAVES *WAVE) void w4a16_gemv_dot2_kernel(
     const uint8_t *cp = codes + static_cast<size_t>(tile) * groups * 512 + h * 512 + j * 16;
     const uint32_t *sp = reinterpret_cast<const uint32_t *>(scales) + static_cast<size_t>(tile) * groups * 16 + h * 16 + r0;
     uint16_t *xw = xs[wave];
+    float *xsw = xsum[wave];
 
     uint32_t magic = 0x64006400u;
     asm volatile("" : "+v"(magic));  // kept in a VGPR: lets the insert be one v_bfi_b32
@@ -344,10 +347,20 @@ __global__ __launch_bounds__(DOT2_WAVES *WAVE) void w4a16_gemv_dot2_kernel(
             c[u] = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(cp + static_cast<size_t>(g) * 512));
             sc[u] = __builtin_nontemporal_load(reinterpret_cast<const v2u *>(sp + static_cast<size_t>(g) * 16));
         }
+        // X per (row, group, lane chunk pair): the slice's chunk sums (dot2
+        // against ones), chunk q + 4's taken from lane ^ 4 (the same row and
+        // group), so the lanes of the products read it instead of summing
+        // their 16 inputs again.  Slots 4..7 and the clamped lanes' values
+        // are never read.
 #pragma unroll
         for (int e = 0; e < XR; ++e) {
             const int i = min(lane + e * WAVE, XC - 1);
             reinterpret_cast<uint4 *>(xw)[i] = xv[e];
+            float t = __builtin_amdgcn_fdot2(one2, __builtin_bit_cast(v2h, xv[e].x), 0.f, false);
+            t = __builtin_amdgcn_fdot2(one2, __builtin_bit_cast(v2h, xv[e].y), t, false);
+            t = __builtin_amdgcn_fdot2(one2, __builtin_bit_cast(v2h, xv[e].z), t, false);
+            t = __builtin_amdgcn_fdot2(one2, __builtin_bit_cast(v2h, xv[e].w), t, false);
+            xsw[i] = t + __shfl_xor(t, 4);
         }
         // The slice is the wave's own: its LDS stores are complete once
         // lgkmcnt drains, and the wave barrier keeps the reads after them.
@@ -379,13 +392,13 @@ __global__ __launch_bounds__(DOT2_WAVES *WAVE) void w4a16_gemv_dot2_kernel(
                 const uint4 x0 = *reinterpret_cast<const uint4 *>(xr);
                 const uint4 x1 = *reinterpret_cast<const uint4 *>(xr + 32);
                 const uint32_t xwd[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-                float pa = 0.f, pb = 0.f, xl = 0.f;
+                const float xl = xsw[(r * FB + 2 * u + h) * 8 + q];
+                float pa = 0.f, pb = 0.f;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     const v2h xq = __builtin_bit_cast(v2h, xwd[i]);
                     pa = __builtin_amdgcn_fdot2(a[i], xq, pa, false);
                     pb = __builtin_amdgcn_fdot2(b[i], xq, pb, false);
-                    xl = __builtin_amdgcn_fdot2(one2, xq, xl, false);
                 }
                 ya[r] = __builtin_fmaf(ma, xl, __builtin_fmaf(sa, pa, ya[r]));
                 yb[r] = __builtin_fmaf(mb, xl, __builtin_fmaf(sb, pb, yb[r]));
