@@ -176,6 +176,35 @@ __global__ __launch_bounds__(WM *WAVE) void w4a16_gemm_kernel(
 // the reference's value for every group of the wave; otherwise a rare
 // uniform branch replaces them with the reference's fp32 fma + RNE before
 // they are used.
+// Activation fragment f = step * TM + i of a group: rows 16 i .. 16 i + 15
+// of the LDS slot, inputs 32 step + 8q .. + 7 (chunks XOR-swizzled by row).
+template <int TM>
+__device__ __forceinline__ void w4a16_read_x(const uint8_t *xs, int f, int r16, int q, v8h (&xr)[2 * TM]) {
+    const int st = f / TM, row = 16 * (f % TM) + r16;
+    xr[f] = *reinterpret_cast<const v8h *>(xs + row * 128 + ((4 * st + q) ^ (row & 7)) * 16);
+}
+
+// The group's MFMAs: fragment f's read LA fragments ahead, the first LA
+// already requested by the caller.
+template <int TM, int TN>
+__device__ __forceinline__ void w4a16_steps(const uint8_t *xs, const uint32_t (&w0)[TN][4],
+                                            const uint32_t (&w1)[TN][4], int r16, int q, v8h (&xr)[2 * TM],
+                                            v4f (&acc)[TN][TM]) {
+    constexpr int NF = 2 * TM, LA = NF < 4 ? NF : 4;
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        if (f + LA < NF) w4a16_read_x<TM>(xs, f + LA, r16, q, xr);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const uint32_t *w = f < TM ? w0[j] : w1[j];
+            acc[j][f % TM] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                __builtin_bit_cast(v8h, uint4{w[0], w[1], w[2], w[3]}), xr[f], acc[j][f % TM], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 template <int TM, int TN>
 __device__ __forceinline__ void w4a16_group_mfma(const uint8_t *xs, const v2i (&c)[TN], const uint32_t (&sc)[TN],
                                                  int r16, int q, v4f (&acc)[TN][TM]) {
@@ -223,30 +252,36 @@ __device__ __forceinline__ void w4a16_group_mfma(const uint8_t *xs, const v2i (&
     // 4096 x 3072 x 12288 296 -> 277 us).
     constexpr int NF = 2 * TM, LA = NF < 4 ? NF : 4;
     v8h xr[NF];
-    auto read_x = [&](int f) {
-        const int st = f / TM, row = 16 * (f % TM) + r16;
-        xr[f] = *reinterpret_cast<const v8h *>(xs + row * 128 + ((4 * st + q) ^ (row & 7)) * 16);
-    };
 #pragma unroll
-    for (int f = 0; f < LA; ++f) read_x(f);
+    for (int f = 0; f < LA; ++f) w4a16_read_x<TM>(xs, f, r16, q, xr);
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) w1[j][i] = word(j, 1, i);
     if (!fast) exact_words(1, w1);
     __builtin_amdgcn_sched_barrier(0);
+    w4a16_steps<TM, TN>(xs, w0, w1, r16, q, xr, acc);
+}
+
+// The same group step on weights dequantised beforehand (fp16 fragments,
+// w[j][step] = the A operand of tile j's MFMA for K step `step`).
+template <int TM, int TN>
+__device__ __forceinline__ void w4a16_group_mfma_f16w(const uint8_t *xs, const v4i (&w)[TN][2], int r16, int q,
+                                                      v4f (&acc)[TN][TM]) {
+    constexpr int NF = 2 * TM, LA = NF < 4 ? NF : 4;
+    v8h xr[NF];
 #pragma unroll
-    for (int f = 0; f < NF; ++f) {
-        if (f + LA < NF) read_x(f + LA);
-        __builtin_amdgcn_sched_barrier(0);
+    for (int f = 0; f < LA; ++f) w4a16_read_x<TM>(xs, f, r16, q, xr);
+    uint32_t w0[TN][4], w1[TN][4];
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const uint32_t *w = f < TM ? w0[j] : w1[j];
-            acc[j][f % TM] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                __builtin_bit_cast(v8h, uint4{w[0], w[1], w[2], w[3]}), xr[f], acc[j][f % TM], 0, 0, 0);
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            w0[j][i] = static_cast<uint32_t>(w[j][0][i]);
+            w1[j][i] = static_cast<uint32_t>(w[j][1][i]);
         }
-        __builtin_amdgcn_sched_barrier(0);
-    }
+    __builtin_amdgcn_sched_barrier(0);
+    w4a16_steps<TM, TN>(xs, w0, w1, r16, q, xr, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -272,7 +307,7 @@ __device__ __forceinline__ void w4a16_group_mfma(const uint8_t *xs, const v2i (&
 // Dequantisation uses packed fp16 (two weights per instruction) when that is
 // provably the reference's value for the group's (scale, minimum), and the
 // reference's fp32 fma + RNE otherwise.
-template <int TM, int TN, int NW, int NSTAGE>
+template <int TM, int TN, int NW, int NSTAGE, bool F16W>
 __global__ __launch_bounds__(NW *WAVE, (NW >= 8 ? 1 : 2)) void w4a16_tiled_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
     const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int m, int n, int k, int n_part,
@@ -296,7 +331,10 @@ __global__ __launch_bounds__(NW *WAVE, (NW >= 8 ? 1 : 2)) void w4a16_tiled_kerne
     const int block_row = tm * BM, block_col = tn * BN;
 
     const uint32_t x_bytes = static_cast<uint32_t>(m) * static_cast<uint32_t>(k) * 2u;
-    const uint32_t c_bytes = static_cast<uint32_t>(n) * static_cast<uint32_t>(k / 2);
+    // F16W: `codes` holds the weights dequantised beforehand, fp16 MFMA
+    // fragments [n / 16][groups][64 lanes][2 steps][8], 2 KiB per tile and
+    // group; `scales` is unused.
+    const uint32_t c_bytes = static_cast<uint32_t>(n) * static_cast<uint32_t>(F16W ? 2 * k : k / 2);
     const uint32_t s_bytes = static_cast<uint32_t>(n) * static_cast<uint32_t>(groups) * 4u;
     const auto rx = buffer_rsrc(x, x_bytes);
     const auto rc = buffer_rsrc(codes, c_bytes);
@@ -319,12 +357,15 @@ __global__ __launch_bounds__(NW *WAVE, (NW >= 8 ? 1 : 2)) void w4a16_tiled_kerne
     for (int j = 0; j < TN; ++j) {
         const int tile = block_col / 16 + wave * TN + j;
         const bool ok = tile < n / 16;
-        c_vo[j] = ok ? static_cast<uint32_t>(tile) * groups * 512u + lane * 8u : c_bytes;
+        c_vo[j] = ok ? (F16W ? static_cast<uint32_t>(tile) * groups * 2048u + lane * 32u
+                             : static_cast<uint32_t>(tile) * groups * 512u + lane * 8u)
+                     : c_bytes;
         s_vo[j] = ok ? static_cast<uint32_t>(tile) * groups * 64u + r16 * 4u : s_bytes;
     }
 
     v2i c_ring[NSTAGE][TN];
     uint32_t s_ring[NSTAGE][TN];
+    v4i w_ring[NSTAGE][TN][2];
     auto issue = [&](int g, int slot) {
 #pragma unroll
         for (int u = 0; u < A_PER_W; ++u) {
@@ -333,8 +374,13 @@ __global__ __launch_bounds__(NW *WAVE, (NW >= 8 ? 1 : 2)) void w4a16_tiled_kerne
         }
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            c_ring[slot][j] = __builtin_amdgcn_raw_buffer_load_b64(rc, c_vo[j], g * 512, 0);
-            s_ring[slot][j] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, s_vo[j], g * 64, 0));
+            if constexpr (F16W) {
+                w_ring[slot][j][0] = __builtin_amdgcn_raw_buffer_load_b128(rc, c_vo[j], g * 2048, 0);
+                w_ring[slot][j][1] = __builtin_amdgcn_raw_buffer_load_b128(rc, c_vo[j] + 16u, g * 2048, 0);
+            } else {
+                c_ring[slot][j] = __builtin_amdgcn_raw_buffer_load_b64(rc, c_vo[j], g * 512, 0);
+                s_ring[slot][j] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, s_vo[j], g * 64, 0));
+            }
         }
     };
 
@@ -345,7 +391,10 @@ __global__ __launch_bounds__(NW *WAVE, (NW >= 8 ? 1 : 2)) void w4a16_tiled_kerne
         for (int i = 0; i < TM; ++i) acc[j][i] = v4f{0.f, 0.f, 0.f, 0.f};
 
     auto compute = [&](int slot) {
-        w4a16_group_mfma<TM, TN>(&lds_a[slot][0][0], c_ring[slot], s_ring[slot], r16, q, acc);
+        if constexpr (F16W)
+            w4a16_group_mfma_f16w<TM, TN>(&lds_a[slot][0][0], w_ring[slot], r16, q, acc);
+        else
+            w4a16_group_mfma<TM, TN>(&lds_a[slot][0][0], c_ring[slot], s_ring[slot], r16, q, acc);
     };
 
     // Prologue: groups 0 .. NSTAGE-2 in flight.  Loads are issued
@@ -451,7 +500,36 @@ static int launch_splitk_reduce(const float *ws, int splits, const float *bias, 
     return launch_status();
 }
 
-template <int TM, int TN, int NW, int NSTAGE = 4>
+// Pre-pass of the fp16-weight path: the tiled codes of n rows dequantised
+// once into the MFMA fragments the tiled kernel reads
+// ([n / 16][groups][64 lanes][2 steps][8] fp16), with the reference's values
+// (packed fp16 where the single rounding is provably the reference's double
+// one, its fp32 fma + RNE otherwise).  One thread per lane of a tile group.
+__global__ __launch_bounds__(256) void w4a16_expand_kernel(const uint8_t *__restrict__ codes,
+                                                           const uint16_t *__restrict__ scales,
+                                                           uint4 *__restrict__ out, long long lanes) {
+    const long long t = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= lanes) return;
+    const long long tg = t >> 6;  // tile * groups + group
+    const int lane = static_cast<int>(t & 63);
+    const uint2 c = *reinterpret_cast<const uint2 *>(codes + tg * 512 + lane * 8);
+    const uint32_t sm = *reinterpret_cast<const uint32_t *>(scales + tg * 32 + (lane & 15) * 2);
+    const uint32_t sb = sm & 0xFFFFu, mb = sm >> 16;
+    const bool fast = w4a16_single_rounding_exact(sb, mb);
+    out[2 * t] = w4a16_dequant8(c.x, sb, mb, fast);
+    out[2 * t + 1] = w4a16_dequant8(c.y, sb, mb, fast);
+}
+
+static int launch_expand(const void *codes, const void *scales, void *out, int n, int k, hipStream_t stream) {
+    const long long lanes = static_cast<long long>(n / 16) * (k / 64) * 64;
+    const long long blocks = (lanes + 255) / 256;
+    if (blocks > 0x7FFFFFFFLL) return kInvalid;
+    w4a16_expand_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(
+        static_cast<const uint8_t *>(codes), static_cast<const uint16_t *>(scales), static_cast<uint4 *>(out), lanes);
+    return launch_status();
+}
+
+template <int TM, int TN, int NW, int NSTAGE = 4, bool F16W = false>
 static int launch_tiled(const void *x, const void *codes, const void *scales, const float *bias, void *y,
                         int out_type, int epi, int m, int n, int k, int n_part, OutMap out, int m_split,
                         hipStream_t stream, int splits = 1, float *ws = nullptr) {
@@ -468,7 +546,7 @@ static int launch_tiled(const void *x, const void *codes, const void *scales, co
     if (blocks > 0x7FFFFFFFLL) return kInvalid;
     if (splits > 1) {
         // Partials into the workspace, then one reduction with the epilogue.
-        w4a16_tiled_kernel<TM, TN, NW, NSTAGE>
+        w4a16_tiled_kernel<TM, TN, NW, NSTAGE, F16W>
             <<<dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(splits)), dim3(NW * WAVE), 0, stream>>>(
                 static_cast<const uint16_t *>(x), static_cast<const uint8_t *>(codes),
                 static_cast<const uint16_t *>(scales), nullptr, ws, QI_HIP_OUT_F32, QI_HIP_EPILOGUE_NONE, m, n, k, n,
@@ -476,7 +554,7 @@ static int launch_tiled(const void *x, const void *codes, const void *scales, co
         if (const int st = launch_status()) return st;
         return launch_splitk_reduce(ws, splits, bias, y, out_type, epi, m, n, n_part, out, stream);
     }
-    w4a16_tiled_kernel<TM, TN, NW, NSTAGE><<<dim3(static_cast<unsigned>(blocks)), dim3(NW * WAVE), 0, stream>>>(
+    w4a16_tiled_kernel<TM, TN, NW, NSTAGE, F16W><<<dim3(static_cast<unsigned>(blocks)), dim3(NW * WAVE), 0, stream>>>(
         static_cast<const uint16_t *>(x), static_cast<const uint8_t *>(codes), static_cast<const uint16_t *>(scales),
         bias, y, out_type, epi, m, n, k, n_part, out, gd);
     return launch_status();
@@ -668,6 +746,10 @@ QI_API int qi_w4a16_gemm(const void *x_half, const void *codes, const void *scal
 
 namespace qi {
 
+#ifndef QI_W4A16_F16W_MIN_M
+#define QI_W4A16_F16W_MIN_M 2048
+#endif
+
 // Kernel shape for m > 16 rows and n_out outputs per stream (measured on
 // MI355X): 1 K-split 64 x 64, 3 tiled 64 x 64, 4 tiled 128 x 192, 5 tiled
 // 256 x 256, 6 tiled 128 x 128 (2, tiled 32 x 64, is no longer chosen).
@@ -747,12 +829,25 @@ static bool w4a16_one_launch(int cfg, int m, int m_split, int n_out) {
     return (t0 + t1 + slots - 1) / slots == (t0 + slots - 1) / slots;
 }
 
-// Workspace a call needs for its K splits (0: none).  A dual call split
-// into two launches runs them in stream order, so they share it.
+// The fp16-weight path: with many rows every weight would be dequantised
+// once per row tile (m / 128 or m / 256 times), so the weights are
+// dequantised once into the workspace (n k fp16) and the tiled kernel reads
+// fp16 fragments instead of codes.
+static bool w4a16_use_f16w(int cfg, int m, int rows, int k) {
+    return (cfg == 4 || cfg == 5 || cfg == 6) && m >= QI_W4A16_F16W_MIN_M &&
+           static_cast<long long>(rows) * k * 2 < (1LL << 32);
+}
+
+// Workspace a call needs for its K splits or its fp16 weights (0: none).  A
+// dual call split into two launches runs them in stream order, so they
+// share it.
 static size_t w4a16_workspace(int m, int m_split, int n_out, int k) {
-    if (m_split <= 0) return splitk_bytes(m, n_out, k);
-    if (w4a16_one_launch(select_w4a16_tiles(m, n_out), m, m_split, n_out)) return 0;
-    const size_t a = splitk_bytes(m_split, n_out, k), b = splitk_bytes(m - m_split, n_out, k);
+    const int cfg = select_w4a16_tiles(m, n_out);
+    if (m_split <= 0)
+        return w4a16_use_f16w(cfg, m, n_out, k) ? static_cast<size_t>(n_out) * k * 2 : splitk_bytes(m, n_out, k);
+    if (w4a16_one_launch(cfg, m, m_split, n_out))
+        return w4a16_use_f16w(cfg, m, 2 * n_out, k) ? static_cast<size_t>(2 * n_out) * k * 2 : 0;
+    const size_t a = w4a16_workspace(m_split, 0, n_out, k), b = w4a16_workspace(m - m_split, 0, n_out, k);
     return a > b ? a : b;
 }
 
@@ -785,6 +880,24 @@ static int dispatch_w4a16(const void *x, const void *codes, const void *scales, 
         if (splits > 1 && static_cast<size_t>(splits) * m * n * 4 <= ws_bytes)
             return launch_tiled<4, 1, 4>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, 0, s,
                                          splits, ws);
+    }
+    if (ws && w4a16_use_f16w(cfg, m, n, k) && static_cast<size_t>(n) * k * 2 <= ws_bytes) {
+        if (const int st = launch_expand(codes, scales, ws, n, k, s)) return st;
+#ifdef QI_W4A16_F16W_TILE  // tile-sweep builds only (TM, TN, NW, NSTAGE); never in the product library
+        return launch_tiled<QI_W4A16_F16W_TILE, true>(x, ws, nullptr, bias, y, out_type, epi, m, n, k, n_part, out,
+                                                      m_split, s);
+#endif
+        switch (cfg) {
+        case 4:
+            return launch_tiled<8, 3, 4, 4, true>(x, ws, nullptr, bias, y, out_type, epi, m, n, k, n_part, out,
+                                                  m_split, s);
+        case 5:
+            return launch_tiled<16, 2, 8, 4, true>(x, ws, nullptr, bias, y, out_type, epi, m, n, k, n_part, out,
+                                                   m_split, s);
+        default:
+            return launch_tiled<8, 2, 4, 4, true>(x, ws, nullptr, bias, y, out_type, epi, m, n, k, n_part, out,
+                                                  m_split, s);
+        }
     }
     switch (cfg) {
     case 1:

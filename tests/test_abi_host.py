@@ -132,7 +132,7 @@ def test_fp6_tile_choice(m, n, cfg):
 @pytest.mark.parametrize("m,m_split,n,k,slices", [
     (300, 0, 1024, 3584, 3), (300, 0, 3584, 3584, 3), (300, 0, 3584, 18944, 3), (300, 0, 37888, 3584, 0),
     (256, 0, 3072, 12288, 4), (256, 0, 3072, 3072, 0), (64, 0, 3072, 12288, 12), (512, 0, 3072, 12288, 2),
-    (4096, 0, 3072, 3072, 0), (4096, 0, 12288, 3072, 0), (16, 0, 3072, 12288, 0),
+    (1536, 0, 3072, 3072, 0), (1536, 0, 12288, 3072, 0), (16, 0, 3072, 12288, 0),
 ])
 def test_w4a16_split_choice(m, m_split, n, k, slices):
     """K slices the W4A16 call with a workspace chooses (workspace bytes =
@@ -141,12 +141,25 @@ def test_w4a16_split_choice(m, m_split, n, k, slices):
     assert qwen_image_hip.load().qi_hip_w4a16_workspace_bytes(m, m_split, n, k) == slices * m * n * 4
 
 
+@pytest.mark.parametrize("m,n,k,f16w", [
+    (4096, 3072, 3072, True), (4096, 12288, 3072, True), (2048, 9216, 3072, True), (4096, 3072, 12288, True),
+    (2047, 9216, 3072, False), (1536, 12288, 3072, False), (1152, 18432, 3072, False),
+])
+def test_w4a16_f16w_choice(m, n, k, f16w):
+    """From 2048 rows (128 x 192, 256 x 256 and 128 x 128 tiles) a call with
+    a workspace dequantises the weights once into it (n k fp16) instead of
+    once per row tile."""
+    assert qwen_image_hip.load().qi_hip_w4a16_workspace_bytes(m, 0, n, k) == (n * k * 2 if f16w else 0)
+
+
 def test_w4a16_split_choice_dual():
-    """A dual call run as two launches needs the larger stream's workspace;
-    one launch over both streams splits nothing."""
+    """A dual call run as two launches needs the larger stream's workspace:
+    here the image stream's fp16 weights (against the text stream's four K
+    slices, 256 x 3072 x 4 x 4 bytes, at K = 12288)."""
     L = qwen_image_hip.load()
-    assert L.qi_hip_w4a16_workspace_bytes(4352, 4096, 3072, 12288) == 4 * 256 * 3072 * 4
-    assert L.qi_hip_w4a16_workspace_bytes(4352, 4096, 9216, 3072) == 0
+    assert L.qi_hip_w4a16_workspace_bytes(4352, 4096, 3072, 12288) == 3072 * 12288 * 2
+    assert L.qi_hip_w4a16_workspace_bytes(4352, 4096, 9216, 3072) == 9216 * 3072 * 2
+    assert L.qi_hip_w4a16_workspace_bytes(1280, 1024, 3072, 12288) == 0  # one launch, 64 x 64 tiles
     assert L.qi_hip_w4a16_workspace_bytes(4352, 4352, 3072, 3072) == 0  # invalid m_split
 
 

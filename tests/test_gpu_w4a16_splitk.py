@@ -8,6 +8,11 @@ workspace-free entry (same tolerance: only the summation order differs),
 for the bias + GELU epilogue, fp16 and fp32 output, the parts layout of a
 fused record, both streams of a dual call, run-to-run identity, and a
 workspace too small for the split (then bit-identical to the unsplit call).
+
+From 2048 rows the workspace instead holds the weights dequantised once to
+fp16 (the reference's values, in the order the tiled kernel reads them):
+the same MFMAs in the same order, so the outputs equal the workspace-free
+call's bit for bit.
 """
 import numpy as np
 import pytest
@@ -90,13 +95,14 @@ def test_w4a16_splitk_f16_parts(dev):
 
 def test_w4a16_splitk_dual(dev):
     """Both streams of the block's MLP down (4096 + 256 rows, 12288 -> 3072):
-    two launches, the text stream's split K; the image stream's rows equal
-    the unsplit call bit for bit, the text rows match the oracle."""
+    two launches, the image stream's on fp16 weights dequantised into the
+    workspace, the text stream's split K; the image stream's rows equal the
+    workspace-free call bit for bit, the text rows match the oracle."""
     import qwen_image_hip as q
     import qwen_image_hip.ops as ops
     m_img, m_txt, n, k = 4096, 256, 3072, 12288
     m = m_img + m_txt
-    assert q.load().qi_hip_w4a16_workspace_bytes(m, m_img, n, k) == 4 * m_txt * n * 4
+    assert q.load().qi_hip_w4a16_workspace_bytes(m, m_img, n, k) == n * k * 2
     x = normal_f16_dev(m, k, 90, dev)
     qw0, tc0, ts0 = _record(n, k, 91, dev)
     qw1, tc1, ts1 = _record(n, k, 92, dev)
@@ -126,3 +132,28 @@ def test_w4a16_splitk_small_workspace(dev):
                                              _ptr(ws), need - 16, _stream())
     assert st == 0
     assert torch.equal(y, ops.w4a16_gemm(x, tc, ts, split_k=False))
+
+
+# (m, n, k, tile choice): 128 x 192, 256 x 256 and 128 x 128 tiles, a
+# ragged last row tile.
+F16W_CASES = [(2048, 9216, 3072, 4), (4096, 12288, 3072, 5), (2048, 2176, 1024, 6), (3000, 12288, 3072, 4)]
+
+
+@pytest.mark.parametrize("m,n,k,cfg", F16W_CASES)
+def test_w4a16_f16w(dev, m, n, k, cfg):
+    import qwen_image_hip as q
+    import qwen_image_hip.ops as ops
+    print(f"w4a16 fp16-weight path m={m} n={n} k={k}", flush=True)
+    L = q.load()
+    assert L.qi_hip_w4a16_tiles(m, n) == cfg
+    assert L.qi_hip_w4a16_workspace_bytes(m, 0, n, k) == n * k * 2
+    x = normal_f16_dev(m, k, 60 + m, dev)
+    qw, tc, ts = _record(n, k, 61 + n, dev)
+    g = torch.Generator(device=dev).manual_seed(m * n)
+    bias = torch.randn(n, generator=g, device=dev)
+    y = ops.w4a16_gemm(x, tc, ts, bias=bias, gelu=True, out_dtype=torch.float16)
+    y_ref = ops.w4a16_gemm(x, tc, ts, bias=bias, gelu=True, out_dtype=torch.float16, split_k=False)
+    assert torch.equal(y, y_ref)
+    rows = sample_rows(m, m + n)
+    _close(_rows_host(y, rows).astype(np.float32), _want(x, rows, qw, bias, gelu=True),
+           f"fp16 weights vs oracle, {len(rows)} rows")
