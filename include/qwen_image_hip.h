@@ -156,18 +156,23 @@ int qi_hip_w4a16_gemm_tiled_dual(const void *x_half, const void *w_tiled_codes, 
  * (short m: the text stream, an encoder's prompt rows), the call splits K
  * over workgroups: fp32 partial tiles go to the workspace, and a second
  * kernel adds them in a fixed order (so results do not depend on timing)
- * and applies the epilogue.  Outputs agree with the workspace-free entries
- * within the W4A16 tolerance (bit for bit when no split is chosen).
- * workspace: 16-byte aligned device memory of workspace_bytes, used only
- * while the call's kernels run on `stream` (calls on one stream may share
- * it); with less than qi_hip_w4a16_workspace_bytes(m, m_split, n, k) the
- * call runs unsplit.  No counterpart in the reference, whose one W4A16
- * kernel has a fixed tile and no K split (gemm.cu:191-268). */
+ * and applies the epilogue.  From 2048 rows per stream (128 x 192,
+ * 256 x 256 and 128 x 128 tiles) the workspace instead receives the
+ * weights dequantised once to fp16 (n k * 2 bytes, the reference's
+ * values), which the tiled kernel reads in place of the codes.  Outputs
+ * agree with the workspace-free entries within the W4A16 tolerance (bit for
+ * bit when no split is chosen).  workspace: 16-byte aligned device memory
+ * of workspace_bytes, used only while the call's kernels run on `stream`
+ * (calls on one stream may share it); with less than
+ * qi_hip_w4a16_workspace_bytes(m, m_split, n, k) the call runs as the
+ * workspace-free entry does.  No counterpart in the reference, whose one
+ * W4A16 kernel has a fixed tile, no K split and dequantises in its loop
+ * (gemm.cu:191-268). */
 int qi_hip_w4a16_gemm_tiled_ws(const void *x_half, const void *w_tiled_codes, const void *w_tiled_scales,
                                const float *bias, void *y, int out_type, int epilogue, int m, int m_split, int n,
                                int k, int n_part, void *workspace, long long workspace_bytes, void *stream);
 /* Workspace bytes the call above uses for (m, m_split, n, k); 0 when it
- * splits no K (or the arguments are invalid).  A query only: no device
+ * needs none (or the arguments are invalid).  A query only: no device
  * work. */
 long long qi_hip_w4a16_workspace_bytes(int m, int m_split, int n, int k);
 
