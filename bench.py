@@ -295,13 +295,27 @@ def device_peaks():
             "hbm_gb_s_published": PEAK_HBM / 1e9}
 
 
+WARM_S = 0.05  # untimed work before every timed region: the clock drops while the GPU idles between sections
+
+
 def time_fn(fn, iters, warmup):
     """Mean ms per call with HIP events on the current stream (the one every
-    op is launched on)."""
+    op is launched on), after `warmup` untimed calls and at least WARM_S
+    seconds of untimed calls (the GPU clock settles again after the host-side
+    set-up between sections)."""
+    import time
+
     import torch
 
     for _ in range(warmup):
         fn()
+    torch.cuda.synchronize()
+    t0, n = time.perf_counter(), 0
+    while time.perf_counter() - t0 < WARM_S and n < 10000:
+        fn()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
