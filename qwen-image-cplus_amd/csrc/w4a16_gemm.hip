@@ -746,6 +746,12 @@ QI_API int qi_w4a16_gemm(const void *x_half, const void *codes, const void *scal
 
 namespace qi {
 
+#ifndef QI_W4A16_S160_MIN_M
+#define QI_W4A16_S160_MIN_M 256
+#endif
+#ifndef QI_W4A16_S160_MIN_GROUPS
+#define QI_W4A16_S160_MIN_GROUPS 128
+#endif
 #ifndef QI_W4A16_F16W_MIN_M
 #define QI_W4A16_F16W_MIN_M 2048
 #endif
@@ -809,7 +815,23 @@ static int select_w4a16_splits(int m, int n_out, int k) {
     return s > 1 ? s : 1;
 }
 
+// Short M with a long K (an encoder's MLP down, 300 x 3584 x 18944): 160-row
+// tiles (every weight dequantised for up to 160 rows instead of 64) with K
+// split into as many slices as keep the launch within two workgroups per
+// CU (their LDS ring is 80 KiB).  Measured on MI355X: 300 x 3584 x 18944
+// 74.7 -> 58.6 us (2 x 56 tiles, 4 slices; 5 slices, one workgroup past a
+// round, 80.7).  0: not used.
+static int select_w4a16_splits160(int m, int n_out, int k) {
+    const int groups = k / 64;
+    if (m <= QI_W4A16_S160_MIN_M || m > 320 || groups < QI_W4A16_S160_MIN_GROUPS) return 0;
+    const long long tiles = static_cast<long long>((m + 159) / 160) * ((n_out + 63) / 64);
+    const long long s = 2LL * device_cus() / tiles;
+    if (s < 2) return 0;
+    return static_cast<int>(s < groups / 16 ? s : groups / 16);
+}
+
 static size_t splitk_bytes(int m, int n_out, int k) {
+    if (const int s160 = select_w4a16_splits160(m, n_out, k)) return static_cast<size_t>(s160) * m * n_out * 4;
     const int s = select_w4a16_splits(m, n_out, k);
     return s > 1 ? static_cast<size_t>(s) * m * n_out * 4 : 0;
 }
@@ -876,6 +898,10 @@ static int dispatch_w4a16(const void *x, const void *codes, const void *scales, 
                               OutMap{out.row_base + m_split, out.m_out, n_out}, 0, s, ws, ws_bytes);
     }
     if (m_split == 0 && ws) {
+        const int s160 = select_w4a16_splits160(m, n_out, k);
+        if (s160 > 1 && static_cast<size_t>(s160) * m * n * 4 <= ws_bytes)
+            return launch_tiled<10, 1, 4>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, 0, s,
+                                          s160, ws);
         const int splits = select_w4a16_splits(m, n_out, k);
         if (splits > 1 && static_cast<size_t>(splits) * m * n * 4 <= ws_bytes)
             return launch_tiled<4, 1, 4>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, 0, s,

@@ -50,7 +50,9 @@ def _want(x, rows, qw, bias=None, gelu=False):
 # (m, n, k, expected slices): slices = workspace / (m * n * 4)
 SPLIT_CASES = [
     (300, 1024, 3584, 3),    # encoder k + v (fused), 80 tiles
-    (300, 3584, 18944, 3),   # encoder down, K = 18944
+    (300, 3584, 18944, 4),   # encoder down, K = 18944: 160-row tiles, 2 x 56 tiles
+    (288, 3584, 9472, 4),    # 160-row tiles, ragged second row tile
+    (320, 3072, 12288, 5),   # 160-row tiles, 2 x 48 tiles
     (256, 3072, 12288, 4),   # text-stream MLP down
     (64, 3072, 12288, 12),   # 48 tiles, long K
     (200, 2048, 8192, 6),    # ragged last row tile
