@@ -746,12 +746,6 @@ QI_API int qi_w4a16_gemm(const void *x_half, const void *codes, const void *scal
 
 namespace qi {
 
-#ifndef QI_W4A16_S160_MIN_M
-#define QI_W4A16_S160_MIN_M 256
-#endif
-#ifndef QI_W4A16_S160_MIN_GROUPS
-#define QI_W4A16_S160_MIN_GROUPS 128
-#endif
 #ifndef QI_W4A16_F16W_MIN_M
 #define QI_W4A16_F16W_MIN_M 2048
 #endif
@@ -815,23 +809,29 @@ static int select_w4a16_splits(int m, int n_out, int k) {
     return s > 1 ? s : 1;
 }
 
-// Short M with a long K (an encoder's MLP down, 300 x 3584 x 18944): 160-row
-// tiles (every weight dequantised for up to 160 rows instead of 64) with K
-// split into as many slices as keep the launch within two workgroups per
-// CU (their LDS ring is 80 KiB).  Measured on MI355X: 300 x 3584 x 18944
-// 74.7 -> 58.6 us (2 x 56 tiles, 4 slices; 5 slices, one workgroup past a
-// round, 80.7).  0: not used.
-static int select_w4a16_splits160(int m, int n_out, int k) {
+// Short M with a long K (an encoder's MLP down, 300 x 3584 x 18944; the text
+// stream's MLP down, 256 x 3072 x 12288): tall tiles -- 128 rows for 161 to
+// 256 rows, 160 for 257 to 320, 64 columns -- so each weight is dequantised
+// for more rows, with K split into as many slices as keep the launch within
+// two workgroups per CU.  Measured on MI355X (us, 64 x 64 split -> tall):
+// 300 x 3584 x 18944 74.7 -> 58.9 (4 slices; 5 slices, one workgroup past a
+// round, 80.7), 320 x 3072 x 12288 43.5 -> 39.2, 256 x 3072 x 12288 34.4 ->
+// 32.6, 200 x 3072 x 12288 32.8 -> 30.5; slower below 128 groups (256 x 3072
+// x 3072 16.0 -> 19.6) and at 160 rows or fewer (no gain).  Returns the
+// slices (0: not used) and the tile's 16-row blocks in tm.
+static int select_w4a16_tall(int m, int n_out, int k, int &tm) {
     const int groups = k / 64;
-    if (m <= QI_W4A16_S160_MIN_M || m > 320 || groups < QI_W4A16_S160_MIN_GROUPS) return 0;
-    const long long tiles = static_cast<long long>((m + 159) / 160) * ((n_out + 63) / 64);
+    tm = m > 256 ? 10 : 8;
+    if (m <= 160 || m > 320 || groups < 128) return 0;
+    const long long tiles = static_cast<long long>((m + 16 * tm - 1) / (16 * tm)) * ((n_out + 63) / 64);
     const long long s = 2LL * device_cus() / tiles;
     if (s < 2) return 0;
     return static_cast<int>(s < groups / 16 ? s : groups / 16);
 }
 
 static size_t splitk_bytes(int m, int n_out, int k) {
-    if (const int s160 = select_w4a16_splits160(m, n_out, k)) return static_cast<size_t>(s160) * m * n_out * 4;
+    int tm;
+    if (const int st = select_w4a16_tall(m, n_out, k, tm)) return static_cast<size_t>(st) * m * n_out * 4;
     const int s = select_w4a16_splits(m, n_out, k);
     return s > 1 ? static_cast<size_t>(s) * m * n_out * 4 : 0;
 }
@@ -898,10 +898,15 @@ static int dispatch_w4a16(const void *x, const void *codes, const void *scales, 
                               OutMap{out.row_base + m_split, out.m_out, n_out}, 0, s, ws, ws_bytes);
     }
     if (m_split == 0 && ws) {
-        const int s160 = select_w4a16_splits160(m, n_out, k);
-        if (s160 > 1 && static_cast<size_t>(s160) * m * n * 4 <= ws_bytes)
-            return launch_tiled<10, 1, 4>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, 0, s,
-                                          s160, ws);
+        int tm;
+        const int st = select_w4a16_tall(m, n_out, k, tm);
+        if (st > 1 && static_cast<size_t>(st) * m * n * 4 <= ws_bytes) {
+            if (tm == 8)
+                return launch_tiled<8, 1, 4>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, 0, s, st,
+                                             ws);
+            return launch_tiled<10, 1, 4>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, 0, s, st,
+                                          ws);
+        }
         const int splits = select_w4a16_splits(m, n_out, k);
         if (splits > 1 && static_cast<size_t>(splits) * m * n * 4 <= ws_bytes)
             return launch_tiled<4, 1, 4>(x, codes, scales, bias, y, out_type, epi, m, n, k, n_part, out, 0, s,

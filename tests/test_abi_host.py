@@ -132,7 +132,7 @@ def test_fp6_tile_choice(m, n, cfg):
 @pytest.mark.parametrize("m,m_split,n,k,slices", [
     (300, 0, 1024, 3584, 3), (300, 0, 3584, 3584, 3), (300, 0, 3584, 18944, 4), (300, 0, 37888, 3584, 0),
     (288, 0, 3584, 9472, 4), (320, 0, 3072, 12288, 5),
-    (256, 0, 3072, 12288, 4), (256, 0, 3072, 3072, 0), (64, 0, 3072, 12288, 12), (512, 0, 3072, 12288, 2),
+    (256, 0, 3072, 12288, 5), (256, 0, 3072, 3072, 0), (64, 0, 3072, 12288, 12), (512, 0, 3072, 12288, 2),
     (1536, 0, 3072, 3072, 0), (1536, 0, 12288, 3072, 0), (16, 0, 3072, 12288, 0),
 ])
 def test_w4a16_split_choice(m, m_split, n, k, slices):

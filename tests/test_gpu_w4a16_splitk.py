@@ -53,9 +53,9 @@ SPLIT_CASES = [
     (300, 3584, 18944, 4),   # encoder down, K = 18944: 160-row tiles, 2 x 56 tiles
     (288, 3584, 9472, 4),    # 160-row tiles, ragged second row tile
     (320, 3072, 12288, 5),   # 160-row tiles, 2 x 48 tiles
-    (256, 3072, 12288, 4),   # text-stream MLP down
+    (256, 3072, 12288, 5),   # text-stream MLP down: 128-row tiles, 2 x 48 tiles
     (64, 3072, 12288, 12),   # 48 tiles, long K
-    (200, 2048, 8192, 6),    # ragged last row tile
+    (200, 2048, 8192, 8),    # 128-row tiles, ragged last row tile
 ]
 
 
