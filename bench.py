@@ -590,14 +590,13 @@ def bench_attention(iters=20):
 
 
 ENCODER_ROWS = 300  # config 4: prompt tokens through the Qwen2.5-VL-7B-shaped text encoder
-ENCODER_SHAPES = [("q", 3584, 3584), ("k+v fused", 2 * 512, 3584), ("gate+up fused", 2 * 18944, 3584),
-                  ("down", 3584, 18944)]
+ENCODER_SHAPES = [("q+k+v fused", 3584 + 2 * 512, 3584), ("gate+up fused", 2 * 18944, 3584), ("down", 3584, 18944)]
 
 
 def bench_encoder(iters=30):
-    """Config 4's encoder linears, W4A16 g64 at M=300 (k and v, gate and up as
-    fused records: one input each), fp16 in / fp16 out; per linear us and the
-    total fp16 TFLOP/s."""
+    """Config 4's encoder linears, W4A16 g64 at M=300 (q, k and v, gate and up
+    as fused records: one input each), fp16 in / fp16 out; per linear us and
+    the total fp16 TFLOP/s."""
     import torch
     import qwen_image_hip as q
     from qwen_image_hip import ops

@@ -93,6 +93,8 @@ W4A16_CASES = [
     (1152, 1024, 256, 6),     # 128 x 128 tiles
     (1152, 18432, 128, 4),    # 128 x 192 tiles, two groups
     (300, 32768, 512, 7),     # 64 x 128 tiles (an encoder's gate + up shape), ragged rows
+    (300, 4608, 3584, 3),     # an encoder's fused q + k + v (3 K slices with a workspace)
+    (300, 3584, 18944, 3),    # an encoder's MLP down (160 x 64 tiles, 4 K slices, with a workspace)
 ]
 
 
