@@ -504,28 +504,28 @@ static int launch_splitk_reduce(const float *ws, int splits, const float *bias, 
 // once into the MFMA fragments the tiled kernel reads
 // ([n / 16][groups][64 lanes][2 steps][8] fp16), with the reference's values
 // (packed fp16 where the single rounding is provably the reference's double
-// one, its fp32 fma + RNE otherwise).  One thread per lane of a tile group.
+// one, its fp32 fma + RNE otherwise).  One thread per 16-byte fragment half
+// (lane, step) of a tile group, so both the 4-byte code reads and the
+// 16-byte stores of consecutive threads are contiguous.
 __global__ __launch_bounds__(256) void w4a16_expand_kernel(const uint8_t *__restrict__ codes,
                                                            const uint16_t *__restrict__ scales,
-                                                           uint4 *__restrict__ out, long long lanes) {
+                                                           uint4 *__restrict__ out, long long halves) {
     const long long t = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (t >= lanes) return;
-    const long long tg = t >> 6;  // tile * groups + group
-    const int lane = static_cast<int>(t & 63);
-    const uint2 c = *reinterpret_cast<const uint2 *>(codes + tg * 512 + lane * 8);
+    if (t >= halves) return;
+    const long long tg = t >> 7;  // tile * groups + group
+    const int lane = static_cast<int>((t >> 1) & 63), step = static_cast<int>(t & 1);
+    const uint32_t c = *reinterpret_cast<const uint32_t *>(codes + tg * 512 + lane * 8 + step * 4);
     const uint32_t sm = *reinterpret_cast<const uint32_t *>(scales + tg * 32 + (lane & 15) * 2);
     const uint32_t sb = sm & 0xFFFFu, mb = sm >> 16;
-    const bool fast = w4a16_single_rounding_exact(sb, mb);
-    out[2 * t] = w4a16_dequant8(c.x, sb, mb, fast);
-    out[2 * t + 1] = w4a16_dequant8(c.y, sb, mb, fast);
+    out[t] = w4a16_dequant8(c, sb, mb, w4a16_single_rounding_exact(sb, mb));
 }
 
 static int launch_expand(const void *codes, const void *scales, void *out, int n, int k, hipStream_t stream) {
-    const long long lanes = static_cast<long long>(n / 16) * (k / 64) * 64;
-    const long long blocks = (lanes + 255) / 256;
+    const long long halves = static_cast<long long>(n / 16) * (k / 64) * 128;
+    const long long blocks = (halves + 255) / 256;
     if (blocks > 0x7FFFFFFFLL) return kInvalid;
     w4a16_expand_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(
-        static_cast<const uint8_t *>(codes), static_cast<const uint16_t *>(scales), static_cast<uint4 *>(out), lanes);
+        static_cast<const uint8_t *>(codes), static_cast<const uint16_t *>(scales), static_cast<uint4 *>(out), halves);
     return launch_status();
 }
 
