@@ -222,12 +222,6 @@ __global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_kernel(
                     if (key >= visible) s[t][r] = -__builtin_inff();
                 }
         }
-        float mx = -__builtin_inff();
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         constexpr int VLA = 4;
         v8h_t vf[16];
         auto read_v = [&](int f) {
@@ -239,37 +233,53 @@ __global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_kernel(
 #pragma unroll
         for (int f = 0; f < VLA; ++f) read_v(f);
         __builtin_amdgcn_sched_barrier(0);
-        // The offset moves only when the tile's maximum exceeds it by more
-        // than 2^8 (exp2 domain), so O and the sum are rarely rescaled: the
-        // probabilities stay <= 256, exact in fp16's normal range as
-        // relative values, and O / sum is unchanged in exact arithmetic.
-        const float new_m = mx > m_run + 8.f ? mx : m_run;
-        // A row with nothing visible yet keeps a zero offset (all its p are 0).
-        const float base = new_m == -__builtin_inff() ? 0.f : new_m;
-        // The hardware exp2 (v_exp_f32): results below 2^-126 flush to zero,
-        // which changes p only where it is already below fp16's range and
-        // the row sum by less than 2^-120.
+        // p = exp2(s - offset) with the running offset first (a row with
+        // nothing visible yet takes 0: all its p are 0).  The hardware exp2
+        // (v_exp_f32): results below 2^-126 flush to zero, which changes p
+        // only where it is already below fp16's range and the row sum by
+        // less than 2^-120.
         float lsum = 0.f;
         v8h_t pb[2][2];  // P^T B operands: tile t, 16-key step e
+        auto probabilities = [&](float base) {
+            lsum = 0.f;
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+            for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float p = __builtin_amdgcn_exp2f(s[t][r] - base);
-                lsum += p;
-                pb[t][r >> 3][r & 7] = static_cast<_Float16>(p);
-            }
-        // alpha is exactly 1 for rows whose offset stayed.
-        if (__any(new_m != m_run)) {
-            const float alpha = __builtin_amdgcn_exp2f(m_run - base);
+                for (int r = 0; r < 16; ++r) {
+                    const float p = __builtin_amdgcn_exp2f(s[t][r] - base);
+                    lsum += p;
+                    pb[t][r >> 3][r & 7] = static_cast<_Float16>(p);
+                }
+        };
+        const float base0 = m_run == -__builtin_inff() ? 0.f : m_run;
+        probabilities(base0);
+        // The offset moves only when some lane's 32 probabilities sum past
+        // 2^8 (so every p stays <= 256: exact in fp16's normal range as
+        // relative values, and O / sum is unchanged in exact arithmetic), or
+        // while a row has no offset yet: then to the rows' exact maximum,
+        // with O and the sum rescaled and the probabilities formed again.
+        // No maximum is taken otherwise.
+        if (__any(!(lsum <= 256.f) || m_run == -__builtin_inff())) {
+            float mx = -__builtin_inff();
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float new_m = mx > m_run ? mx : m_run;
+            const float base = new_m == -__builtin_inff() ? 0.f : new_m;
+            probabilities(base);
+            // alpha is exactly 1 for rows whose offset stayed; O and the sum
+            // so far were formed at offset base0.
+            const float alpha = __builtin_amdgcn_exp2f(base0 - base);
             l_run *= alpha;
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
+            m_run = new_m;
         }
         l_run += lsum;
-        m_run = new_m;
         // O^T += V^T P^T.  Step (t, e) covers keys 32t + 16e + 8(i / 4) +
         // 4h + i % 4 in K slot 8h + i: from the V^T row of dim d, the runs
         // of 4 keys at 32t + 16e + 4h and 32t + 16e + 8 + 4h.  MFMA f = 4j
