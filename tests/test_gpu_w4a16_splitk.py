@@ -159,3 +159,31 @@ def test_w4a16_f16w(dev, m, n, k, cfg):
     rows = sample_rows(m, m + n)
     _close(_rows_host(y, rows).astype(np.float32), _want(x, rows, qw, bias, gelu=True),
            f"fp16 weights vs oracle, {len(rows)} rows")
+
+
+# Ragged shapes on each workspace path: tall 128-row and 160-row K splits
+# (rows 161..320, >= 128 groups) and the fp16-weight path on 128 x 128 tiles
+# with a ragged last row tile -- against the oracle on sampled rows and the
+# workspace-free entry (bit for bit on the fp16-weight path).
+RAGGED_CASES = [(161, 1024, 8192, "tall"), (255, 2048, 8192, "tall"), (257, 1024, 8192, "tall"),
+                (319, 512, 16384, "tall"), (2085, 1408, 1024, "f16w"), (2085, 1408, 3072, "f16w")]
+
+
+@pytest.mark.parametrize("m,n,k,path", RAGGED_CASES)
+def test_w4a16_workspace_paths_ragged(dev, m, n, k, path):
+    import qwen_image_hip as q
+    import qwen_image_hip.ops as ops
+    print(f"w4a16 workspace path {path} m={m} n={n} k={k}", flush=True)
+    ws = q.load().qi_hip_w4a16_workspace_bytes(m, 0, n, k)
+    # fp16 weights (n k halves), or whole fp32 K slices of the output.
+    assert ws == n * k * 2 if path == "f16w" else (ws > 0 and ws % (m * n * 4) == 0)
+    x = normal_f16_dev(m, k, 3 * m + k, dev)
+    qw, tc, ts = _record(n, k, m + n, dev)
+    y = ops.w4a16_gemm(x, tc, ts)
+    y_ref = ops.w4a16_gemm(x, tc, ts, split_k=False)
+    if path == "f16w":
+        assert torch.equal(y, y_ref)
+    else:
+        _close(y.cpu().numpy(), y_ref.cpu().numpy(), "split vs unsplit, all rows")
+    rows = sample_rows(m, m + k)
+    _close(_rows_host(y, rows), _want(x, rows, qw), f"vs oracle, {len(rows)} rows")
