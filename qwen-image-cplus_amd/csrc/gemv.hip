@@ -296,14 +296,21 @@ __global__ __launch_bounds__(GEMV_WAVES *WAVE) void w4a16_gemv_factored_kernel(
 // tolerance, and are bit-exact fp32(c s + min) on one-hot rows.  (Using the
 // reference's fp16 weights here, exact double rounding included, measured
 // 1.35x slower on the all-blocks launch.)
-constexpr int DOT2_WAVES = 8;
-constexpr int DOT2_FB = 6;  // groups per wave and chunk: three 16-byte loads per lane
-
-template <int M>
-__global__ __launch_bounds__(DOT2_WAVES *WAVE) void w4a16_gemv_dot2_kernel(
+// W waves per workgroup (one 16-row tile), FB groups per wave and chunk
+// (FB / 2 16-byte loads per lane; FB even).  Measured on MI355X (us, W 8
+// FB 6 -> W 4 FB 4): every block's modulation linears as one fused record
+// (120 matrices, 138240 tiles) at m = 1 693 -> 641, at m = 2 901 -> 770;
+// one 3072 -> 18432 matrix 8.5 -> 8.6 (m = 1), 10.3 -> 10.1 (m = 2).  (W 4
+// FB 6 was as fast fused and W 2 FB 6 slower on one matrix; one shape for
+// every launch keeps a fused record's outputs bit-identical to per-matrix
+// calls.)
+constexpr int DOT2_WAVES = 4, DOT2_FB = 4;
+template <int M, int W, int FB>
+__global__ __launch_bounds__(W *WAVE) void w4a16_gemv_dot2_kernel(
     const uint16_t *__restrict__ x, const uint8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
     const float *__restrict__ bias, void *__restrict__ y, int out_type, int epi, int n, int k, int n_part) {
-    constexpr int W = DOT2_WAVES, FB = DOT2_FB, NI = FB / 2;
+    static_assert(FB % 2 == 0, "two groups per 16-byte load");
+    constexpr int NI = FB / 2;
     constexpr int XC = M * FB * 8;  // 16-byte chunks of a wave's x slice
     constexpr int XR = (XC + WAVE - 1) / WAVE;
     __shared__ float partial[W][4][M][16];
@@ -438,10 +445,11 @@ static void launch_gemv(const uint16_t *x, const uint8_t *c, const uint16_t *s, 
     const dim3 grid(static_cast<unsigned>(n / 16)), block(GEMV_WAVES * WAVE);
     const long long lds = static_cast<long long>(m) * k * 2;
     // One or two rows: the vector-unit form (its LDS does not grow with k).
+    constexpr int W = DOT2_WAVES, FB = DOT2_FB;
     if (m == 1)
-        w4a16_gemv_dot2_kernel<1><<<grid, dim3(DOT2_WAVES * WAVE), 0, stream>>>(x, c, s, bias, y, out_type, epi, n, k, n_part);
+        w4a16_gemv_dot2_kernel<1, W, FB><<<grid, dim3(W * WAVE), 0, stream>>>(x, c, s, bias, y, out_type, epi, n, k, n_part);
     else if (m == 2)
-        w4a16_gemv_dot2_kernel<2><<<grid, dim3(DOT2_WAVES * WAVE), 0, stream>>>(x, c, s, bias, y, out_type, epi, n, k, n_part);
+        w4a16_gemv_dot2_kernel<2, W, FB><<<grid, dim3(W * WAVE), 0, stream>>>(x, c, s, bias, y, out_type, epi, n, k, n_part);
     else if (lds <= GEMV_LDS_X)
         w4a16_gemv_factored_kernel<<<grid, block, static_cast<size_t>(lds), stream>>>(x, c, s, bias, y, out_type, epi,
                                                                                       m, n, k, n_part);

@@ -190,7 +190,7 @@ def test_w4a16_epilogue_f16_bias_gelu(dev, gelu):
 
 
 # m = 1, 2 also at group counts that leave waves idle (1, 13 groups) or a
-# ragged last chunk (56, 100 groups over eight waves of six-group chunks).
+# ragged last chunk (56, 100 groups over four waves of four-group chunks).
 @pytest.mark.parametrize("m,n,k", [(1, 18432, 3072), (2, 18432, 3072), (3, 64, 256), (16, 512, 3584 // 64 * 64),
                                    (1, 96, 64), (2, 160, 832), (1, 48, 6400), (2, 32, 3584)])
 def test_w4a16_gemv(dev, m, n, k):
