@@ -746,9 +746,8 @@ QI_API int qi_w4a16_gemm(const void *x_half, const void *codes, const void *scal
 
 namespace qi {
 
-#ifndef QI_W4A16_F16W_MIN_M
-#define QI_W4A16_F16W_MIN_M 2048
-#endif
+// Rows from which a call with a workspace runs on fp16 weights.
+constexpr int W4A16_F16W_MIN_M = 2048;
 
 // Kernel shape for m > 16 rows and n_out outputs per stream (measured on
 // MI355X): 1 K-split 64 x 64, 3 tiled 64 x 64, 4 tiled 128 x 192, 5 tiled
@@ -856,7 +855,7 @@ static bool w4a16_one_launch(int cfg, int m, int m_split, int n_out) {
 // dequantised once into the workspace (n k fp16) and the tiled kernel reads
 // fp16 fragments instead of codes.
 static bool w4a16_use_f16w(int cfg, int m, int rows, int k) {
-    return (cfg == 4 || cfg == 5 || cfg == 6) && m >= QI_W4A16_F16W_MIN_M &&
+    return (cfg == 4 || cfg == 5 || cfg == 6) && m >= W4A16_F16W_MIN_M &&
            static_cast<long long>(rows) * k * 2 < (1LL << 32);
 }
 
@@ -914,10 +913,6 @@ static int dispatch_w4a16(const void *x, const void *codes, const void *scales, 
     }
     if (ws && w4a16_use_f16w(cfg, m, n, k) && static_cast<size_t>(n) * k * 2 <= ws_bytes) {
         if (const int st = launch_expand(codes, scales, ws, n, k, s)) return st;
-#ifdef QI_W4A16_F16W_TILE  // tile-sweep builds only (TM, TN, NW, NSTAGE); never in the product library
-        return launch_tiled<QI_W4A16_F16W_TILE, true>(x, ws, nullptr, bias, y, out_type, epi, m, n, k, n_part, out,
-                                                      m_split, s);
-#endif
         switch (cfg) {
         case 4:
             return launch_tiled<8, 3, 4, 4, true>(x, ws, nullptr, bias, y, out_type, epi, m, n, k, n_part, out,
