@@ -415,8 +415,9 @@ def gemv_only():
 
 def w4a16_only():
     """The fp16-MFMA kernel's counter workload: the image stream's W4A16 MLP
-    up linear (4096 x 12288 x 3072, GELU-tanh, fp16 out) x 11 (the last 10
-    timed), then a plain 512 MiB copy x 5 for the counter calibration."""
+    up linear (4096 x 12288 x 3072, GELU-tanh, fp16 out): one call, untimed
+    calls for at least WARM_S seconds, 10 timed calls, then a plain 512 MiB
+    copy x 5 for the counter calibration."""
     import torch
     import qwen_image_hip as q
     from qwen_image_hip import ops
@@ -441,7 +442,7 @@ def w4a16_only():
         dst.copy_(src)
     torch.cuda.synchronize()
     total = n * k // 2 + n * (k // 64) * 4 + m * k * 2 + m * n * 2
-    log(f"w4a16-only: 1 + 10 x W4A16 GEMM m={m} n={n} k={k} gelu fp16 out ({total} algorithmic bytes, "
+    log(f"w4a16-only: W4A16 GEMM m={m} n={n} k={k} gelu fp16 out ({total} algorithmic bytes, "
         f"{2 * m * n * k} flops), {ms * 1e3:.1f} us per launch by HIP events over the 10; 5 x copy 536870912 B")
     return 0
 
