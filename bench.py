@@ -381,8 +381,9 @@ def kernel_only():
 def gemv_only():
     """The HBM-bound kernel's counter workload: all 60 blocks' modulation
     linears (image + text stream, 120 x 3072->18432, m = 1) as one fused GEMV
-    launch x 11 (the last 10 timed), then a plain 512 MiB copy x 5 whose known byte count
-    calibrates the FETCH_SIZE / WRITE_SIZE counters."""
+    launch: one, untimed launches for at least WARM_S seconds, 10 timed, then a
+    plain 512 MiB copy x 5 whose known byte count calibrates the FETCH_SIZE /
+    WRITE_SIZE counters."""
     import torch
     import qwen_image_hip as q
     from qwen_image_hip import ops
@@ -408,7 +409,7 @@ def gemv_only():
         dst.copy_(src)
     torch.cuda.synchronize()
     total = parts * (n * k // 2 + n * (k // 64) * 4) + k * 2 + parts * n * 2
-    log(f"gemv-only: 1 + 10 x fused modulation GEMV m=1 n={parts}x{n} k={k} ({total} algorithmic bytes), "
+    log(f"gemv-only: fused modulation GEMV m=1 n={parts}x{n} k={k} ({total} algorithmic bytes), "
         f"{ms * 1e3:.1f} us per launch by HIP events over the 10; 5 x copy 536870912 B")
     return 0
 
