@@ -159,16 +159,17 @@ __device__ __forceinline__ void fp6_tiles(uint8_t *lds, const uint8_t *__restric
     // next lane's codes, or bytes past the buffer, which read as zero; they
     // land in the slot's unused fourth dword.
     const uint32_t lds0 = lds_address(lds);
-    auto issue = [&](int g, int slot) {
+    auto issue_one = [&](int g, int slot, int u) {
 #ifdef QI_ABLATE_DMA
         return;
 #endif
+        const int H = H0 + u;
+        dma_dwordx4(H < 2 * MT ? ra : rw, lds0 + slot * SLOT + (H >> 1) * TILE + (H & 1) * 1024, vo[u],
+                    sbase[u] + g * BLOCK);
+    };
+    auto issue = [&](int g, int slot) {
 #pragma unroll
-        for (int u = 0; u < L_PER_W; ++u) {
-            const int H = H0 + u;
-            dma_dwordx4(H < 2 * MT ? ra : rw, lds0 + slot * SLOT + (H >> 1) * TILE + (H & 1) * 1024, vo[u],
-                        sbase[u] + g * BLOCK);
-        }
+        for (int u = 0; u < L_PER_W; ++u) issue_one(g, slot, u);
     };
 
     v16f acc[TN][TM];
@@ -354,7 +355,6 @@ __device__ __forceinline__ void fp6_tiles(uint8_t *lds, const uint8_t *__restric
         __builtin_amdgcn_s_barrier();
 #endif
         asm volatile("" ::: "memory");
-        issue(gload, u);
         if constexpr (!LAST) read_frags(std::integral_constant<int, (u + 1) % NSTAGE>{}, F);
         __builtin_amdgcn_sched_barrier(0);
         // Tile q = i * TN + j.  Its next partial tile is issued LAG tiles
@@ -366,6 +366,15 @@ __device__ __forceinline__ void fp6_tiles(uint8_t *lds, const uint8_t *__restric
             if constexpr (q < T) {
                 constexpr int i = q / TN, j = q % TN;
                 tile_fma(j, i);
+                __builtin_amdgcn_sched_barrier(0);
+                // The next group's DMA loads go out one per tile step so their
+                // issue cost overlaps the MFMA chain instead of stalling it at
+                // the group's start; the vmcnt wait per group is unchanged.
+                if constexpr (q < L_PER_W) issue_one(gload, u, q);
+                if constexpr (q == T - 1) {
+#pragma unroll
+                    for (int uu = T; uu < L_PER_W; ++uu) issue_one(gload, u, uu);
+                }
                 __builtin_amdgcn_sched_barrier(0);
                 // sp[i] is free once the last tile of row tile i has
                 // stepped.
