@@ -46,7 +46,7 @@ extern "C" {
 #endif
 
 /* ABI version of this header; bumped on any signature change. */
-#define QI_HIP_ABI_VERSION 4
+#define QI_HIP_ABI_VERSION 5
 int qi_hip_abi_version(void);
 
 /* ---------------------------------------------------------------------------
@@ -305,6 +305,29 @@ int qi_flash_attention(const float *q, const void *k_half, const void *v_half, f
                        int heads, int query_offset, int causal_rows, const int *visible_keys);
 int qi_hip_flash_attention(const float *q, const void *k_half, const void *v_half, float *out, int queries, int keys,
                            int heads, int query_offset, int causal_rows, const int *visible_keys, void *stream);
+/* The attention above with a caller workspace.  A call in which every row
+ * sees every key (visible_keys NULL and causal_rows <= query_offset)
+ * balances the work over one workgroup per CU: each walks an equal share
+ * of the (head, 256-query block, 64-key tile) sequence, and where a
+ * workgroup's share ends inside a query block, its O, offset and sum go to
+ * the workspace and the block's last part to finish merges the parts in
+ * workgroup order (so results do not depend on timing).  Outputs agree
+ * with qi_hip_flash_attention within the attention tolerance.  Masked
+ * calls, calls the split would not speed up (query blocks a multiple of the
+ * CU count), and calls with less than
+ * qi_hip_flash_attention_workspace_bytes(queries, keys, heads) run as
+ * qi_hip_flash_attention does.  workspace: 16-byte aligned device memory
+ * used only while the call's kernels run on `stream` (calls on one stream
+ * may share it; its contents need no initialisation).  No counterpart in
+ * the reference, whose grid is one workgroup per query block and head
+ * (flash.cu:237-244). */
+int qi_hip_flash_attention_ws(const float *q, const void *k_half, const void *v_half, float *out, int queries,
+                              int keys, int heads, int query_offset, int causal_rows, const int *visible_keys,
+                              void *workspace, long long workspace_bytes, void *stream);
+/* Workspace bytes the call above uses for a mask-free call of (queries,
+ * keys, heads) on the current device; 0 when it would not split (or the
+ * arguments are invalid).  A query only: no device work. */
+long long qi_hip_flash_attention_workspace_bytes(int queries, int keys, int heads);
 
 /* Device-side QIPACK quantiser (int4_pack.cplus:237-468 arithmetic, bit-exact):
  * w_half fp16 [n, k] -> QIPACK arrays.  scheme 5 = W4A16 affine (minimums

@@ -27,6 +27,15 @@
 // lane holds, in the MFMA output order, and the V^T fragments (A operand)
 // are read with the same key order from the transposed tile.  O^T lanes also
 // hold one query each, so the online rescaling is lane-local.
+//
+// Balanced split (flash_attention_stream_kernel, mask-free calls with a
+// workspace).  One workgroup fills a CU, so 17 query blocks x 24 heads =
+// 408 workgroups run as 1.6 rounds on 256 CUs.  Instead one workgroup per CU
+// walks an equal share of the (unit, key tile) sequence, units = (head,
+// query block) in head-major order; a unit cut between workgroups leaves
+// each part's O^T, offset and sum in the workspace, and the part that
+// arrives last (an arrival counter per unit) merges them in workgroup order,
+// so the result does not depend on timing.
 
 #include "qi_common.h"
 
@@ -48,45 +57,28 @@ __device__ __forceinline__ int att_visible(int global_row, int keys, int causal_
     return global_row < causal_rows ? global_row + 1 : keys;
 }
 
-__global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_kernel(
-    const float *__restrict__ q, const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
-    float *__restrict__ out, int queries, int keys, int heads, int query_offset, int causal_rows,
-    const int *__restrict__ visible_keys) {
-    __shared__ __attribute__((aligned(16))) uint16_t k_lds2[2][ATT_KT * ATT_KROW];
-    __shared__ __attribute__((aligned(16))) uint16_t vt_lds2[2][ATT_HD * ATT_VROW];
-    __shared__ int wg_visible;
+struct AttLds {
+    __attribute__((aligned(16))) uint16_t k[2][ATT_KT * ATT_KROW];
+    __attribute__((aligned(16))) uint16_t vt[2][ATT_HD * ATT_VROW];
+    int visible;
+    int last;
+};
 
+// Keys [kbegin, kend) of one unit (head, query block `qblk`) for this
+// thread's wave: O^T (o), running offset and sum, from zero.  `visible` is
+// the lane's visible key count, `wmin` the wave's smallest; every thread of
+// the workgroup calls it with the same unit and range (tile staging and
+// barriers are shared), and it returns after a barrier, so the LDS tiles are
+// free again.
+__device__ __forceinline__ void att_keys(const float *__restrict__ q, const uint16_t *__restrict__ k,
+                                         const uint16_t *__restrict__ v, int queries, int keys, int heads, int head,
+                                         int qblk, int kbegin, int kend, int visible, int wmin, AttLds &lds,
+                                         v16f_t (&o)[4], float &m_run, float &l_run) {
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
     const int h = lane >> 5, l32 = lane & 31;
-    int head, qblk;
-    {
-        const int nqb = gridDim.x, nh = gridDim.y;
-        const int id = blockIdx.x + nqb * blockIdx.y, total = nqb * nh;
-        const int xcd = id % 8, slot = id / 8;
-        // The hardware hands workgroup `id` to XCD id % 8; XCD x takes the
-        // linear work items [x * per, (x + 1) * per) of head-major order, so
-        // one head's query blocks share an XCD's L2 (measured 2 % faster).
-        const int per = (total + 7) / 8;
-        int w = xcd * per + slot;
-        if (total % 8 != 0 || w >= total) w = id;  // uneven split: keep the plain order
-        head = w / nqb;
-        qblk = w % nqb;
-    }
     const int width = heads * ATT_HD;
     const int qi = qblk * ATT_QB + wave * 32 + l32;  // this lane's query
     const bool q_ok = qi < queries;
-    const int visible = q_ok ? min(att_visible(qi + query_offset, keys, causal_rows, visible_keys), keys) : 0;
-
-    // How far this workgroup reads: the largest visible count of its rows.
-    if (tid == 0) wg_visible = 0;
-    __syncthreads();
-    int wv = visible;
-#pragma unroll
-    for (int s = 32; s > 0; s >>= 1) wv = max(wv, __shfl_xor(wv, s, 64));
-    if (lane == 0) atomicMax(&wg_visible, wv);
-    __syncthreads();
-    const int limit = wg_visible;
-
     // Q^T fragments (B operand): K-step s holds dims 16s + 8h .. + 7 of the
     // lane's query, scaled into the log2 domain and rounded to fp16.
     const float scale = 1.4426950408889634f / __builtin_sqrtf(static_cast<float>(ATT_HD));
@@ -105,18 +97,12 @@ __global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_kernel(
                       static_cast<_Float16>(b.z * scale), static_cast<_Float16>(b.w * scale)};
     }
 
-    v16f_t o[4];  // O^T: d-tile j, register 4a + b = dim 32j + 8a + 4h + b
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[j][r] = 0.f;
-    float m_run = -__builtin_inff(), l_run = 0.f;
-
-    // The smallest visible count of this wave's queries: tiles below it need
-    // no mask.
-    int wmin = q_ok ? visible : keys;
-#pragma unroll
-    for (int s = 32; s > 0; s >>= 1) wmin = min(wmin, __shfl_xor(wmin, s, 64));
+    m_run = -__builtin_inff();
+    l_run = 0.f;
 
     // Tile staging through registers into the LDS slot not being read: K as
     // 16-byte chunks per thread (row-major), V as a 2-key x 8-dim block per
@@ -153,8 +139,8 @@ __global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_kernel(
         }
     };
     auto store_tile = [&](int buf) {
-        uint16_t *k_lds = k_lds2[buf];
-        uint16_t *vt_lds = vt_lds2[buf];
+        uint16_t *k_lds = lds.k[buf];
+        uint16_t *vt_lds = lds.vt[buf];
 #pragma unroll
         for (int i = 0; i < ATT_KCH; ++i) {
             const int idx = tid + i * ATT_WAVES * WAVE, key = idx >> 4, chunk = idx & 15;
@@ -175,16 +161,16 @@ __global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_kernel(
     // Two LDS slots: tile i is read from slot i % 2 while tile i + 1 (loaded
     // into registers during tile i - 1) is stored into the other after the
     // tile's products; one barrier per tile then orders both.
-    if (limit > 0) {
-        load_tile(0);
+    if (kbegin < kend) {
+        load_tile(kbegin);
         store_tile(0);
         __syncthreads();
-        if (ATT_KT < limit) load_tile(ATT_KT);
+        if (kbegin + ATT_KT < kend) load_tile(kbegin + ATT_KT);
     }
     int buf = 0;
-    for (int start = 0; start < limit; start += ATT_KT, buf ^= 1) {
-        const uint16_t *k_lds = k_lds2[buf];
-        const uint16_t *vt_lds = vt_lds2[buf];
+    for (int start = kbegin; start < kend; start += ATT_KT, buf ^= 1) {
+        const uint16_t *k_lds = lds.k[buf];
+        const uint16_t *vt_lds = lds.vt[buf];
 
         // S^T for the tile's two 32-key halves t: register 4a + b of s[t]
         // holds key start + 32t + 8a + 4h + b of the lane's query.  The two
@@ -293,15 +279,25 @@ __global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_kernel(
             o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[f], pb[t][e], o[j], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
-        if (start + ATT_KT < limit) store_tile(buf ^ 1);
+        if (start + ATT_KT < kend) store_tile(buf ^ 1);
         __syncthreads();
-        if (start + 2 * ATT_KT < limit) load_tile(start + 2 * ATT_KT);
+        if (start + 2 * ATT_KT < kend) load_tile(start + 2 * ATT_KT);
     }
 
-    // Both halves' sums, then O / sum (0 when nothing was visible).
+}
+
+// O / sum for this lane's query (0 when nothing was visible): both key
+// halves' sums, then the lane's 64 dims.  o as att_keys leaves it (O^T
+// register 4a + b of d-tile j = dim 32j + 8a + 4h + b).
+__device__ __forceinline__ void att_store(float *__restrict__ out, const v16f_t (&o)[4], float l_run, int queries,
+                                          int heads, int head, int qblk) {
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    const int h = lane >> 5, l32 = lane & 31;
+    const int width = heads * ATT_HD;
+    const int qi = qblk * ATT_QB + wave * 32 + l32;
     const float total = l_run + __shfl_xor(l_run, 32, 64);
     const float inverse = total > 0.f ? 1.0f / total : 0.f;
-    if (q_ok) {
+    if (qi < queries) {
         float *dst = out + static_cast<size_t>(qi) * width + head * ATT_HD + 4 * h;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -313,19 +309,255 @@ __global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_kernel(
     }
 }
 
-static int launch_attention(const float *q, const void *k, const void *v, float *out, int queries, int keys,
-                            int heads, int query_offset, int causal_rows, const int *visible_keys,
-                            hipStream_t stream) {
+__global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_kernel(
+    const float *__restrict__ q, const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
+    float *__restrict__ out, int queries, int keys, int heads, int query_offset, int causal_rows,
+    const int *__restrict__ visible_keys) {
+    __shared__ AttLds lds;
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    const int l32 = lane & 31;
+    int head, qblk;
+    {
+        const int nqb = gridDim.x, nh = gridDim.y;
+        const int id = blockIdx.x + nqb * blockIdx.y, total = nqb * nh;
+        const int xcd = id % 8, slot = id / 8;
+        // The hardware hands workgroup `id` to XCD id % 8; XCD x takes the
+        // linear work items [x * per, (x + 1) * per) of head-major order, so
+        // one head's query blocks share an XCD's L2 (measured 2 % faster).
+        const int per = (total + 7) / 8;
+        int w = xcd * per + slot;
+        if (total % 8 != 0 || w >= total) w = id;  // uneven split: keep the plain order
+        head = w / nqb;
+        qblk = w % nqb;
+    }
+    const int qi = qblk * ATT_QB + wave * 32 + l32;  // this lane's query
+    const bool q_ok = qi < queries;
+    const int visible = q_ok ? min(att_visible(qi + query_offset, keys, causal_rows, visible_keys), keys) : 0;
+
+    // How far this workgroup reads: the largest visible count of its rows.
+    if (tid == 0) lds.visible = 0;
+    __syncthreads();
+    int wv = visible;
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) wv = max(wv, __shfl_xor(wv, s, 64));
+    if (lane == 0) atomicMax(&lds.visible, wv);
+    __syncthreads();
+    const int limit = lds.visible;
+
+    // The smallest visible count of this wave's queries: tiles below it need
+    // no mask.
+    int wmin = q_ok ? visible : keys;
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) wmin = min(wmin, __shfl_xor(wmin, s, 64));
+
+    v16f_t o[4];
+    float m_run, l_run;
+    att_keys(q, k, v, queries, keys, heads, head, qblk, 0, limit, visible, wmin, lds, o, m_run, l_run);
+    att_store(out, o, l_run, queries, heads, head, qblk);
+}
+
+// Workspace of the balanced split for `parts` workgroups and `units` units:
+// the arrival counters, then per workgroup two part slots (the unit its
+// split range starts in, the unit it ends in) of offsets and sums (float2
+// per thread) and O^T (64 floats per thread, register-major so that each
+// access of a wave is 256 contiguous bytes).
+constexpr int ATT_THREADS = ATT_WAVES * WAVE;
+inline size_t att_counter_bytes(long long units) { return (static_cast<size_t>(units) * 4 + 255) / 256 * 256; }
+inline size_t att_split_bytes(long long units, int parts) {
+    return att_counter_bytes(units) + static_cast<size_t>(2 * parts) * ATT_THREADS * (8 + 64 * 4);
+}
+
+__global__ void att_clear_kernel(unsigned *__restrict__ counters, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) counters[i] = 0u;
+}
+
+// Parts cross workgroups (and XCDs, whose L2s are not coherent with each
+// other) through device-scope atomic stores and loads, which the compiler
+// issues as coherent (sc1) dword accesses: a device-scope fence would write
+// back and invalidate the whole L2 of the XCD instead, evicting the K/V
+// tiles its other workgroups are reading (measured: 24 heads 280 -> 401 us).
+__device__ __forceinline__ void att_put(float *p, float x) {
+    __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float att_get(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One workgroup per CU.  First `rounds` rounds of whole units in lockstep
+// (unit i * parts + r in round i: the workgroups of an XCD then read the
+// same key tiles of the same heads at the same time, as the plain grid
+// does), then the remaining units' key tiles split into equal ranges.
+__global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_stream_kernel(
+    const float *__restrict__ q, const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
+    float *__restrict__ out, int queries, int keys, int heads, unsigned *__restrict__ arrivals,
+    float *__restrict__ part_ml, float *__restrict__ part_o, int rounds, long long total, int nt, int nqb) {
+    __shared__ AttLds lds;
+    const int tid = threadIdx.x;
+    const int parts = gridDim.x;
+    // Ranges in XCD-major order (workgroup id goes to XCD id % 8), so that
+    // neighbouring units and ranges -- the same head's -- share an XCD's L2.
+    const int id = blockIdx.x;
+    const int r = parts % 8 == 0 ? (id % 8) * (parts / 8) + id / 8 : id;
+    for (int i = 0; i < rounds; ++i) {
+        const int u = i * parts + r;
+        v16f_t o[4];
+        float m_run, l_run;
+        att_keys(q, k, v, queries, keys, heads, u / nqb, u % nqb, 0, keys, keys, keys, lds, o, m_run, l_run);
+        att_store(out, o, l_run, queries, heads, u / nqb, u % nqb);
+    }
+    const int ubase = rounds * parts;  // first split unit; t counts its tiles on
+    auto bound = [&](int rr) { return static_cast<long long>(rr) * total / parts; };
+    // The range holding split tile t: the largest rr with bound(rr) <= t.
+    auto owner = [&](long long t) { return static_cast<int>(((t + 1) * parts + total - 1) / total - 1); };
+    const long long t0 = bound(r), t1 = bound(r + 1);
+    for (long long t = t0; t < t1;) {
+        const int us = static_cast<int>(t / nt);
+        const int tb = static_cast<int>(t - static_cast<long long>(us) * nt);
+        const int te = static_cast<int>(min(static_cast<long long>(nt), tb + (t1 - t)));
+        const int u = ubase + us, head = u / nqb, qblk = u % nqb;
+        v16f_t o[4];
+        float m_run, l_run;
+        att_keys(q, k, v, queries, keys, heads, head, qblk, tb * ATT_KT, min(te * ATT_KT, keys), keys, keys, lds, o,
+                 m_run, l_run);
+        t += te - tb;
+        if (tb == 0 && te == nt) {
+            att_store(out, o, l_run, queries, heads, head, qblk);
+            continue;
+        }
+        // A part of unit u: ranges r_first..r_last hold its parts, range rr
+        // in slot 2 rr when its range starts inside u, else 2 rr + 1.
+        const long long ubegin = static_cast<long long>(us) * nt;
+        const int r_first = owner(ubegin), r_last = owner(ubegin + nt - 1);
+        auto slot = [&](int rr) { return bound(rr) >= ubegin ? 2 * rr : 2 * rr + 1; };
+        const int own = slot(r);
+        att_put(part_ml + (2 * own) * ATT_THREADS + tid, m_run);
+        att_put(part_ml + (2 * own + 1) * ATT_THREADS + tid, l_run);
+        float *po = part_o + static_cast<size_t>(own) * 64 * ATT_THREADS + tid;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) att_put(po + (16 * j + e) * ATT_THREADS, o[j][e]);
+        // Every thread's stores complete (acknowledged at the coherent
+        // level), then one arrival; the part that arrives last merges.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0)
+            lds.last = __hip_atomic_fetch_add(&arrivals[u], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                       static_cast<unsigned>(r_last - r_first);
+        __syncthreads();
+        if (!lds.last) continue;
+        float mx = -__builtin_inff();
+        for (int rr = r_first; rr <= r_last; ++rr) mx = fmaxf(mx, att_get(part_ml + (2 * slot(rr)) * ATT_THREADS + tid));
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) o[j][e] = 0.f;
+        float l_sum = 0.f;
+        for (int rr = r_first; rr <= r_last; ++rr) {
+            const int sl = slot(rr);
+            const float m_s = att_get(part_ml + (2 * sl) * ATT_THREADS + tid);
+            const float w = m_s == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m_s - mx);
+            l_sum += w * att_get(part_ml + (2 * sl + 1) * ATT_THREADS + tid);
+            const float *pi = part_o + static_cast<size_t>(sl) * 64 * ATT_THREADS + tid;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) o[j][e] += w * att_get(pi + (16 * j + e) * ATT_THREADS);
+        }
+        att_store(out, o, l_sum, queries, heads, head, qblk);
+    }
+}
+
+static int check_attention(const float *q, const void *k, const void *v, float *out, int queries, int keys,
+                           int heads) {
     if (queries < 0 || keys < 0 || heads <= 0 || heads > 65535) return kInvalid;
-    if (queries == 0) return 0;
-    if (!q || !out || (keys > 0 && (!k || !v))) return kInvalid;
+    if (queries > 0 && (!q || !out || (keys > 0 && (!k || !v)))) return kInvalid;
     if (reinterpret_cast<uintptr_t>(q) % 16 || reinterpret_cast<uintptr_t>(out) % 16 ||
         reinterpret_cast<uintptr_t>(k) % 16 || reinterpret_cast<uintptr_t>(v) % 16)
         return kInvalid;
+    return 0;
+}
+
+static int launch_attention(const float *q, const void *k, const void *v, float *out, int queries, int keys,
+                            int heads, int query_offset, int causal_rows, const int *visible_keys,
+                            hipStream_t stream) {
+    if (const int e = check_attention(q, k, v, out, queries, keys, heads)) return e;
+    if (queries == 0) return 0;
     const dim3 grid(static_cast<unsigned>((queries + ATT_QB - 1) / ATT_QB), static_cast<unsigned>(heads));
-    flash_attention_kernel<<<grid, dim3(ATT_WAVES * WAVE), 0, stream>>>(
+    flash_attention_kernel<<<grid, dim3(ATT_THREADS), 0, stream>>>(
         q, static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v), out, queries, keys, heads,
         query_offset, causal_rows, visible_keys);
+    return launch_status();
+}
+
+// The balanced split's shape for a mask-free call on the current device:
+// `parts` workgroups (one per CU) run `rounds` lockstep rounds of whole
+// units (of `nt` key tiles), then split the remaining units' `total` tiles
+// into equal ranges.  Returns false where that would not save tile steps
+// per CU against the plain grid's whole rounds (units a multiple of the CU
+// count, or too few split tiles for a part's merge to pay).  The CU count
+// is the current device's (256 when no device is visible).
+struct AttSplit {
+    long long units, total;
+    int nt, nqb, parts, rounds;
+};
+static bool attention_split(int queries, int keys, int heads, AttSplit &sp) {
+    if (queries <= 0 || keys <= 0) return false;
+    const int cus = device_cus();
+    sp.nqb = (queries + ATT_QB - 1) / ATT_QB;
+    sp.nt = (keys + ATT_KT - 1) / ATT_KT;
+    sp.units = static_cast<long long>(sp.nqb) * heads;
+    if (sp.units >= (1ll << 31) || sp.units * sp.nt >= (1ll << 40)) return false;
+    sp.rounds = static_cast<int>(sp.units / cus);
+    sp.total = (sp.units - static_cast<long long>(sp.rounds) * cus) * sp.nt;
+    // Every range must hold at least one tile (so each unit's parts are
+    // exactly the ranges r_first..r_last): one part per tile when there
+    // are fewer tiles than CUs and no whole rounds.
+    sp.parts = cus;
+    if (sp.total < cus) {
+        if (sp.rounds > 0 || sp.total == 0) return false;
+        sp.parts = static_cast<int>(sp.total);
+    }
+    const long long plain = (sp.units + cus - 1) / cus * sp.nt;
+    const long long split = sp.rounds * static_cast<long long>(sp.nt) + (sp.total + sp.parts - 1) / sp.parts;
+    // Charge each range two tile steps for its merges; take the split only
+    // where it saves at least 5 % of the plain grid's steps.
+    return (split + 2) * 100 <= plain * 95;
+}
+
+static long long attention_workspace(int queries, int keys, int heads) {
+    AttSplit sp;
+    if (!attention_split(queries, keys, heads, sp)) return 0;
+    return static_cast<long long>(att_split_bytes(sp.units, sp.parts));
+}
+
+static int launch_attention_ws(const float *q, const void *k, const void *v, float *out, int queries, int keys,
+                               int heads, int query_offset, int causal_rows, const int *visible_keys,
+                               void *workspace, long long workspace_bytes, hipStream_t stream) {
+    if (const int e = check_attention(q, k, v, out, queries, keys, heads)) return e;
+    if (workspace_bytes < 0 || reinterpret_cast<uintptr_t>(workspace) % 16) return kInvalid;
+    AttSplit sp;
+    // Only calls where every row sees every key split: no visible_keys and
+    // no causal row among these rows.
+    const bool mask_free = visible_keys == nullptr && causal_rows <= query_offset;
+    if (!mask_free || !workspace || !attention_split(queries, keys, heads, sp) ||
+        workspace_bytes < static_cast<long long>(att_split_bytes(sp.units, sp.parts)))
+        return launch_attention(q, k, v, out, queries, keys, heads, query_offset, causal_rows, visible_keys,
+                                stream);
+    auto *base = static_cast<unsigned char *>(workspace);
+    auto *arrivals = reinterpret_cast<unsigned *>(base);
+    auto *part_ml = reinterpret_cast<float *>(base + att_counter_bytes(sp.units));
+    auto *part_o = reinterpret_cast<float *>(base + att_counter_bytes(sp.units) +
+                                             static_cast<size_t>(2 * sp.parts) * ATT_THREADS * 8);
+    // The counters start at zero on every call (a fill kernel, not a memset,
+    // so the pair can sit in a captured graph).
+    att_clear_kernel<<<static_cast<unsigned>((sp.units + 255) / 256), 256, 0, stream>>>(arrivals,
+                                                                                       static_cast<int>(sp.units));
+    if (const int e = launch_status()) return e;
+    flash_attention_stream_kernel<<<sp.parts, dim3(ATT_THREADS), 0, stream>>>(
+        q, static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v), out, queries, keys, heads, arrivals,
+        part_ml, part_o, sp.rounds, sp.total, sp.nt, sp.nqb);
     return launch_status();
 }
 
@@ -342,4 +574,17 @@ QI_API int qi_hip_flash_attention(const float *q, const void *k_half, const void
                                   void *stream) {
     return qi::launch_attention(q, k_half, v_half, out, queries, keys, heads, query_offset, causal_rows,
                                 visible_keys, qi::stream_of(stream));
+}
+
+QI_API long long qi_hip_flash_attention_workspace_bytes(int queries, int keys, int heads) {
+    if (queries < 0 || keys < 0 || heads <= 0 || heads > 65535) return 0;
+    return qi::attention_workspace(queries, keys, heads);
+}
+
+QI_API int qi_hip_flash_attention_ws(const float *q, const void *k_half, const void *v_half, float *out, int queries,
+                                     int keys, int heads, int query_offset, int causal_rows,
+                                     const int *visible_keys, void *workspace, long long workspace_bytes,
+                                     void *stream) {
+    return qi::launch_attention_ws(q, k_half, v_half, out, queries, keys, heads, query_offset, causal_rows,
+                                   visible_keys, workspace, workspace_bytes, qi::stream_of(stream));
 }

@@ -45,6 +45,7 @@ SIGNATURES: dict[str, list] = {
     "qi_hip_w4a4_fp6_tiles": [_i, _i],
     "qi_flash_attention": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
     "qi_hip_flash_attention": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p],
+    "qi_hip_flash_attention_ws": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p, ctypes.c_longlong, _p],
     "qi_hip_layer_norm_scale": [_p, _p, _i, _p, _i, _i, _i, _i, _p],
     "qi_hip_layer_norm_scale_quantize_fp6": [_p, _p, _i, _i, _p, _p, _i, _i, _p],
     "qi_hip_layer_norm_scale_quantize_fp6_noalloc": [_p, _p, _i, _i, _p, _i, _i, _p],
@@ -60,9 +61,10 @@ SIGNATURES: dict[str, list] = {
 }
 # Entry points whose return type is not int.
 RESTYPES = {"qi_fnv1a": (_u64, [_u64, _p, _u64]), "qi_pack_close": (None, [_p]),
-            "qi_hip_w4a16_workspace_bytes": (ctypes.c_longlong, [_i, _i, _i, _i])}
+            "qi_hip_w4a16_workspace_bytes": (ctypes.c_longlong, [_i, _i, _i, _i]),
+            "qi_hip_flash_attention_workspace_bytes": (ctypes.c_longlong, [_i, _i, _i])}
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lib = None
 

@@ -370,10 +370,13 @@ def swiglu_quantize_fp6(gate: torch.Tensor, up: torch.Tensor, codes6: torch.Tens
 
 def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, heads: int, query_offset: int = 0,
                     causal_rows: int = 0, visible_keys: torch.Tensor | None = None,
-                    out: torch.Tensor | None = None) -> torch.Tensor:
+                    out: torch.Tensor | None = None, balanced: bool = True) -> torch.Tensor:
     """Fused attention, head dim 128 (reference qi_flash_attention,
     qwen_image_cuda/cuda/flash.cu): q fp32 [queries, heads*128], k and v fp16
-    [keys, heads*128]; visible_keys an int32 device tensor indexed by global row."""
+    [keys, heads*128]; visible_keys an int32 device tensor indexed by global row.
+    balanced: mask-free calls spread their key tiles evenly over the CUs
+    (qi_hip_flash_attention_ws, workspace from torch's caching allocator);
+    False runs the one-workgroup-per-query-block grid."""
     nq, width = q.shape
     if q.dtype != torch.float32 or k.dtype != torch.float16 or v.dtype != torch.float16:
         raise TypeError("q fp32, k and v fp16")
@@ -382,6 +385,15 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, heads: in
     if visible_keys is not None and visible_keys.dtype != torch.int32:
         raise TypeError("visible_keys must be int32")
     out = out if out is not None else _empty((nq, width), torch.float32, q)
-    check(load().qi_hip_flash_attention(_ptr(q), _ptr(k), _ptr(v), _ptr(out), nq, k.shape[0], heads, query_offset,
-                                        causal_rows, _ptr(visible_keys), _stream()), "attention")
+    lib = load()
+    mask_free = visible_keys is None and causal_rows <= query_offset
+    ws_bytes = lib.qi_hip_flash_attention_workspace_bytes(nq, k.shape[0], heads) if balanced and mask_free else 0
+    if ws_bytes > 0:
+        ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=q.device)
+        check(lib.qi_hip_flash_attention_ws(_ptr(q), _ptr(k), _ptr(v), _ptr(out), nq, k.shape[0], heads,
+                                            query_offset, causal_rows, None, _ptr(ws), ws_bytes, _stream()),
+              "attention")
+        return out
+    check(lib.qi_hip_flash_attention(_ptr(q), _ptr(k), _ptr(v), _ptr(out), nq, k.shape[0], heads, query_offset,
+                                     causal_rows, _ptr(visible_keys), _stream()), "attention")
     return out

@@ -225,3 +225,28 @@ def test_cplus_binding_matches_the_header():
     assert cplus["qi_w4a4_gemm"][0] == [("a_codes", "*u8"), ("a_scales", "*u8"), ("w_codes", "*u8"),
                                         ("w_scales", "*u8"), ("y", "*f32"), ("m", "i32"), ("n", "i32"), ("k", "i32")]
     assert cplus["qi_f32_to_f16"] == ([("source", "*f32"), ("out", "*u8"), ("count", "u64")], "i32")
+
+
+def _att_split_bytes(units, parts):
+    """Counters (4 bytes per unit, 256-byte rounded), then two part slots per
+    workgroup of 512 threads x (offset, sum, 64 O floats)."""
+    return (units * 4 + 255) // 256 * 256 + 2 * parts * 512 * (8 + 256)
+
+
+@pytest.mark.parametrize("nq,nk,heads,parts", [
+    (4352, 4352, 24, 256),      # 408 query blocks: one lockstep round, 152 blocks split
+    (4352, 4352, 8, 256),       # 136 query blocks: all split
+    (129, 1000, 2, 32),         # 2 blocks x 16 key tiles: one part per tile
+    (4352, 4352, 15, None),     # 255 blocks: one round already
+    (4352, 4352, 30, None),     # 510 blocks: the split would not save 5 %
+    (256 * 256, 4352, 1, None), # exactly one round
+    (0, 64, 1, None), (64, 0, 1, None), (64, 64, 0, None),
+])
+def test_attention_split_choice(nq, nk, heads, parts):
+    """The attention's balanced split (qi_hip_flash_attention_ws) and its
+    workspace at a 256-CU device's rule (the library's default when no GPU
+    is visible): taken where whole rounds of 256-query blocks would leave CUs
+    idle for at least 5 % of the plain grid's tile steps."""
+    got = qwen_image_hip.load().qi_hip_flash_attention_workspace_bytes(nq, nk, heads)
+    units = -(-nq // 256) * heads
+    assert got == (0 if parts is None else _att_split_bytes(units, parts))

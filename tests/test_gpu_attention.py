@@ -100,3 +100,69 @@ def test_attention_full_block_size_vs_torch_fp32(dev):
     p = torch.softmax(s * float(np.log(2.0)), dim=-1)
     want = torch.bmm(p, v.float().view(n, heads, 128).transpose(0, 1)).transpose(0, 1).reshape(n, heads * 128)
     _close(got.cpu().numpy(), want.cpu().numpy())
+
+
+def _split_bytes(nq, nk, heads):
+    import qwen_image_hip
+    return qwen_image_hip.load().qi_hip_flash_attention_workspace_bytes(nq, nk, heads)
+
+
+def test_attention_split_choice(dev):
+    """The balanced split is taken where whole rounds of query blocks would
+    leave CUs idle, and not where the query blocks fill the CUs evenly."""
+    import qwen_image_hip
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    assert _split_bytes(4352, 4352, 24) > 0                    # 408 blocks: 1.6 rounds
+    assert _split_bytes(256 * cus, 4352, 1) == 0               # exactly one round
+    assert _split_bytes(129, 1000, 2) > 0                      # 2 blocks: keys spread over CUs
+    assert _split_bytes(0, 1000, 2) == 0 and _split_bytes(10, 0, 2) == 0
+    assert _split_bytes(10, 10, 0) == 0
+
+
+@pytest.mark.parametrize("nq,nk,heads,offset", [(2000, 600, 40, 0), (300, 4100, 3, 0), (1000, 333, 5, 64)])
+def test_attention_split_vs_oracle(dev, nq, nk, heads, offset):
+    """Parts spanning several query blocks, ragged key and query tiles, and
+    a query offset with no causal row: the balanced split against the
+    oracle and against the one-block-per-workgroup grid."""
+    print(f"attention split nq={nq} nk={nk} heads={heads} offset={offset}", flush=True)
+    assert _split_bytes(nq, nk, heads) > 0
+    q, k, v = _case(nq, nk, heads, 1500 + nq)
+    got = _run(dev, q, k, v, heads, query_offset=offset, causal_rows=offset)
+    plain = _run(dev, q, k, v, heads, query_offset=offset, causal_rows=offset, balanced=False)
+    want = oracle.flash_attention(q, k, v, heads, query_offset=offset, causal_rows=offset)
+    _close(got, want)
+    _close(plain, want)
+    # The parts form their fp16 probabilities at their own offsets, so the
+    # two grids round differently: equal within the attention tolerance.
+    d = rel_l2(got, plain)
+    print(f"  split vs plain rel-L2 {d:.3e}", flush=True)
+    assert d <= REL_L2_TOL
+
+
+def test_attention_split_deterministic_and_small_workspace(dev):
+    """Two balanced calls give identical bits (parts merge in workgroup
+    order, whatever order they finish in); a workspace one byte short runs
+    the plain grid, bit for bit."""
+    import qwen_image_hip
+    from qwen_image_hip import ops
+    L = qwen_image_hip.load()
+    n, heads = 4352, 24
+    g = torch.Generator(device=dev)
+    g.manual_seed(1600)
+    q = torch.randn((n, heads * 128), generator=g, device=dev)
+    k = torch.randn((n, heads * 128), generator=g, device=dev).half()
+    v = torch.randn((n, heads * 128), generator=g, device=dev).half()
+    a = ops.flash_attention(q, k, v, heads)
+    b = ops.flash_attention(q, k, v, heads)
+    plain = ops.flash_attention(q, k, v, heads, balanced=False)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    assert ((a - plain).norm() / plain.norm()).item() <= REL_L2_TOL
+    ws_bytes = L.qi_hip_flash_attention_workspace_bytes(n, n, heads)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+    short = torch.empty_like(q)
+    s = torch.cuda.current_stream().cuda_stream
+    assert L.qi_hip_flash_attention_ws(q.data_ptr(), k.data_ptr(), v.data_ptr(), short.data_ptr(), n, n, heads, 0, 0,
+                                       None, ws.data_ptr(), ws_bytes - 1, s) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(short, plain)
