@@ -232,8 +232,9 @@ __global__ __launch_bounds__(8 * WAVE) void quantize_lane16_kernel(
     constexpr bool HALF = !__is_same(Vals, uint16_t);  // see butterfly4
     constexpr float unit = HALF ? 1.0f : 16.0f;
     constexpr int ROW = 256 + 16;  // floats per LDS row: 16 bytes of padding after every 64 values
-    // The tile's rows, then (once every wave has its values back) the
-    // tile's code blocks in the same bytes: 34 KiB, four workgroups per CU.
+    // The tile's rows (34 KiB) and code blocks (7 KiB): three workgroups
+    // per CU.  Putting the blocks in the rows' bytes after a barrier (four
+    // per CU) measured no faster.
     __shared__ __attribute__((aligned(16))) float rows[32 * ROW];
     __shared__ __attribute__((aligned(16))) uint32_t blocks[4 * FP6_BLOCK / 4];
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
