@@ -816,16 +816,23 @@ static int select_w4a16_splits(int m, int n_out, int k) {
 // 300 x 3584 x 18944 74.7 -> 58.9 (4 slices; 5 slices, one workgroup past a
 // round, 80.7), 320 x 3072 x 12288 43.5 -> 39.2, 256 x 3072 x 12288 34.4 ->
 // 32.6, 200 x 3072 x 12288 32.8 -> 30.5; slower below 128 groups (256 x 3072
-// x 3072 16.0 -> 19.6) and at 160 rows or fewer (no gain).  Returns the
+// x 3072 16.0 -> 19.6) and at 160 rows or fewer (no gain).  From 257 rows
+// (where 64-row tiles leave a partial fifth tile) down to 48 groups while
+// the launch keeps 1.5 workgroups per CU: 300 x 4608 x 3584 (an encoder's
+// fused q, k, v) 29.4 -> 25.5 (432 workgroups); 300 x 3584 x 3584 (336)
+// 24.1 either way, 320 x 3072 x 3072 (288) 20.6 -> 22.6 and 300 x 1024 x
+// 3584 (96) 14.5 -> 17.9, so those keep the 64 x 64 split.  Returns the
 // slices (0: not used) and the tile's 16-row blocks in tm.
 static int select_w4a16_tall(int m, int n_out, int k, int &tm) {
     const int groups = k / 64;
     tm = m > 256 ? 10 : 8;
-    if (m <= 160 || m > 320 || groups < 128) return 0;
+    if (m <= 160 || m > 320 || groups < 48) return 0;
     const long long tiles = static_cast<long long>((m + 16 * tm - 1) / (16 * tm)) * ((n_out + 63) / 64);
     const long long s = 2LL * device_cus() / tiles;
     if (s < 2) return 0;
-    return static_cast<int>(s < groups / 16 ? s : groups / 16);
+    const int st = static_cast<int>(s < groups / 16 ? s : groups / 16);
+    if (groups < 128 && (m <= 256 || tiles * st * 2 < 3LL * device_cus())) return 0;
+    return st;
 }
 
 static size_t splitk_bytes(int m, int n_out, int k) {

@@ -131,6 +131,7 @@ def test_fp6_tile_choice(m, n, cfg):
 
 @pytest.mark.parametrize("m,m_split,n,k,slices", [
     (300, 0, 1024, 3584, 3), (300, 0, 3584, 3584, 3), (300, 0, 3584, 18944, 4), (300, 0, 37888, 3584, 0),
+    (300, 0, 4608, 3584, 3), (320, 0, 3072, 3072, 3),
     (288, 0, 3584, 9472, 4), (320, 0, 3072, 12288, 5),
     (256, 0, 3072, 12288, 5), (256, 0, 3072, 3072, 0), (64, 0, 3072, 12288, 12), (512, 0, 3072, 12288, 2),
     (1536, 0, 3072, 3072, 0), (1536, 0, 12288, 3072, 0), (16, 0, 3072, 12288, 0),

@@ -50,6 +50,7 @@ def _want(x, rows, qw, bias=None, gelu=False):
 # (m, n, k, expected slices): slices = workspace / (m * n * 4)
 SPLIT_CASES = [
     (300, 1024, 3584, 3),    # encoder k + v (fused), 80 tiles
+    (300, 4608, 3584, 3),    # encoder q + k + v (fused), 56 groups: 160-row tiles, 2 x 72 tiles
     (300, 3584, 18944, 4),   # encoder down, K = 18944: 160-row tiles, 2 x 56 tiles
     (288, 3584, 9472, 4),    # 160-row tiles, ragged second row tile
     (320, 3072, 12288, 5),   # 160-row tiles, 2 x 48 tiles
