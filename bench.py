@@ -1044,7 +1044,8 @@ def bench_library(iters=50):
     g = torch.Generator(device="cuda")
     g.manual_seed(99)
     shapes = [(4096, 3 * HIDDEN, HIDDEN), (4096, HIDDEN, HIDDEN), (4096, 4 * HIDDEN, HIDDEN),
-              (4096, HIDDEN, 4 * HIDDEN), (4352, 3 * HIDDEN, HIDDEN)]
+              (4096, HIDDEN, 4 * HIDDEN), (4352, 3 * HIDDEN, HIDDEN), (4352, 4 * HIDDEN, HIDDEN),
+              (4352, HIDDEN, 4 * HIDDEN)]
     out = {}
     for m, n, k in shapes:
         x = torch.randn((m, k), generator=g, device="cuda").half()
