@@ -113,30 +113,43 @@ __device__ __forceinline__ void att_keys(const float *__restrict__ q, const uint
     // V: 32 key pairs x 16 dim blocks of 8 over the workgroup's threads.
     constexpr int ATT_VDB = 16 / (ATT_WAVES * WAVE / 32);  // dim blocks per thread
     uint32_t vn[ATT_VDB][2][4];
-    auto load_tile = [&](int start) {
+    // Buffer loads: a lane's 16-byte chunks sit at fixed byte offsets from
+    // the tile's first row of this head (voffset), the tile's base and
+    // range are scalar, and rows at or past `keys` lie beyond the range, so
+    // they read as zeros with no per-key test or branch.
+    uint32_t k_vo[ATT_KCH], v_vo[ATT_VDB][2];
 #pragma unroll
-        for (int i = 0; i < ATT_KCH; ++i) {
-            const int idx = tid + i * ATT_WAVES * WAVE, key = idx >> 4, chunk = idx & 15;
-            kn[i] = uint4{0u, 0u, 0u, 0u};
-            if (start + key < keys)
-                kn[i] = *reinterpret_cast<const uint4 *>(k + static_cast<size_t>(start + key) * width +
-                                                         head * ATT_HD + chunk * 8);
-        }
+    for (int i = 0; i < ATT_KCH; ++i) {
+        const int idx = tid + i * ATT_WAVES * WAVE, key = idx >> 4, chunk = idx & 15;
+        k_vo[i] = static_cast<uint32_t>(key * width * 2 + chunk * 16);
+    }
 #pragma unroll
-        for (int b = 0; b < ATT_VDB; ++b) {
+    for (int b = 0; b < ATT_VDB; ++b)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
             const int kp = tid & 31, db = (tid >> 5) + b * (ATT_WAVES * WAVE / 32);
+            v_vo[b][r] = static_cast<uint32_t>((2 * kp + r) * width * 2 + 16 * db);
+        }
+    auto load_tile = [&](int start) {
+        // Bytes of this head's rows from `start` on; a tile reads at most
+        // 64 rows (< 2^31 bytes), so clamping the range keeps it exact.
+        const long long left = static_cast<long long>(keys - start) * width * 2 - head * ATT_HD * 2;
+        const uint32_t bytes = static_cast<uint32_t>(left < 0x7FFFFFF0LL ? left : 0x7FFFFFF0LL);
+        const size_t base = static_cast<size_t>(start) * width + head * ATT_HD;
+        const auto rk = buffer_rsrc(k + base, bytes), rv = buffer_rsrc(v + base, bytes);
+#pragma unroll
+        for (int i = 0; i < ATT_KCH; ++i)
+            kn[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, k_vo[i], 0, 0));
+#pragma unroll
+        for (int b = 0; b < ATT_VDB; ++b)
 #pragma unroll
             for (int r = 0; r < 2; ++r) {
-                uint4 t = uint4{0u, 0u, 0u, 0u};
-                const int key = start + 2 * kp + r;
-                if (key < keys)
-                    t = *reinterpret_cast<const uint4 *>(v + static_cast<size_t>(key) * width + head * ATT_HD + 8 * db);
+                const uint4 t = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, v_vo[b][r], 0, 0));
                 vn[b][r][0] = t.x;
                 vn[b][r][1] = t.y;
                 vn[b][r][2] = t.z;
                 vn[b][r][3] = t.w;
             }
-        }
     };
     auto store_tile = [&](int buf) {
         uint16_t *k_lds = lds.k[buf];
