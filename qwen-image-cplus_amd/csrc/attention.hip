@@ -50,7 +50,7 @@ constexpr int ATT_WAVES = 8;          // waves per workgroup, 32 queries each (8
 constexpr int ATT_KCH = ATT_KT * ATT_HD / 8 / (ATT_WAVES * 64);  // K chunks per thread
 constexpr int ATT_QB = ATT_WAVES * 32;
 constexpr int ATT_KROW = ATT_HD + 8;  // K tile row pitch, halves (keeps the 32 rows a fragment read touches apart)
-constexpr int ATT_VROW = ATT_KT + 8;  // V^T tile row pitch, halves
+constexpr int ATT_VROW = ATT_KT + 4;  // V^T tile row pitch, halves (34 dwords: 16 rows, 8-byte reads, distinct banks)
 
 __device__ __forceinline__ int att_visible(int global_row, int keys, int causal_rows, const int *visible_keys) {
     if (visible_keys != nullptr) return visible_keys[global_row];
@@ -229,8 +229,12 @@ __device__ __forceinline__ void att_keys(const float *__restrict__ q, const uint
             const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + 8);
             vf[f] = __builtin_bit_cast(v8h_t, uint4{lo.x, lo.y, hi.x, hi.y});
         };
+        // Issue order g: the d-tile j = g % 4 changes fastest, so that
+        // consecutive MFMAs accumulate into different tiles of O (four
+        // apart) instead of waiting on each other's results.
+        auto pv_f = [](int g) { return 4 * (g & 3) + (g >> 2); };
 #pragma unroll
-        for (int f = 0; f < VLA; ++f) read_v(f);
+        for (int g = 0; g < VLA; ++g) read_v(pv_f(g));
         __builtin_amdgcn_sched_barrier(0);
         // p = exp2(s - offset) with the running offset first (a row with
         // nothing visible yet takes 0: all its p are 0).  The hardware exp2
@@ -285,10 +289,10 @@ __device__ __forceinline__ void att_keys(const float *__restrict__ q, const uint
         // + 2t + e; its V fragment is read VLA MFMAs ahead (the first ones
         // before the softmax, above).
 #pragma unroll
-        for (int f = 0; f < 16; ++f) {
-            if (f + VLA < 16) read_v(f + VLA);
+        for (int g = 0; g < 16; ++g) {
+            if (g + VLA < 16) read_v(pv_f(g + VLA));
             __builtin_amdgcn_sched_barrier(0);
-            const int j = f >> 2, t = (f >> 1) & 1, e = f & 1;
+            const int f = pv_f(g), j = f >> 2, t = (f >> 1) & 1, e = f & 1;
             o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[f], pb[t][e], o[j], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
