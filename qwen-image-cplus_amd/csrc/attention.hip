@@ -402,28 +402,31 @@ __device__ __forceinline__ float att_get(const float *p) {
 }
 
 // One workgroup per CU.  First `rounds` rounds of whole units in lockstep
-// (unit i * parts + r in round i: the workgroups of an XCD then read the
-// same key tiles of the same heads at the same time, as the plain grid
-// does), then the remaining units' key tiles split into equal ranges.
+// (unit i * gridDim.x + r in round i: the workgroups of an XCD then read
+// the same key tiles of the same heads at the same time, as the plain grid
+// does), then the remaining units' key tiles split into `parts` equal
+// ranges, run by ranges 0 .. parts - 1.
 __global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_stream_kernel(
     const float *__restrict__ q, const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     float *__restrict__ out, int queries, int keys, int heads, unsigned *__restrict__ arrivals,
-    float *__restrict__ part_ml, float *__restrict__ part_o, int rounds, long long total, int nt, int nqb) {
+    float *__restrict__ part_ml, float *__restrict__ part_o, int rounds, long long total, int nt, int nqb,
+    int parts) {
     __shared__ AttLds lds;
     const int tid = threadIdx.x;
-    const int parts = gridDim.x;
+    const int wgs = gridDim.x;
     // Ranges in XCD-major order (workgroup id goes to XCD id % 8), so that
     // neighbouring units and ranges -- the same head's -- share an XCD's L2.
     const int id = blockIdx.x;
-    const int r = parts % 8 == 0 ? (id % 8) * (parts / 8) + id / 8 : id;
+    const int r = wgs % 8 == 0 ? (id % 8) * (wgs / 8) + id / 8 : id;
     for (int i = 0; i < rounds; ++i) {
-        const int u = i * parts + r;
+        const int u = i * wgs + r;
         v16f_t o[4];
         float m_run, l_run;
         att_keys(q, k, v, queries, keys, heads, u / nqb, u % nqb, 0, keys, keys, keys, lds, o, m_run, l_run);
         att_store(out, o, l_run, queries, heads, u / nqb, u % nqb);
     }
-    const int ubase = rounds * parts;  // first split unit; t counts its tiles on
+    if (r >= parts) return;              // the split tail runs on ranges 0 .. parts - 1
+    const int ubase = rounds * wgs;  // first split unit; t counts its tiles on
     auto bound = [&](int rr) { return static_cast<long long>(rr) * total / parts; };
     // The range holding split tile t: the largest rr with bound(rr) <= t.
     auto owner = [&](long long t) { return static_cast<int>(((t + 1) * parts + total - 1) / total - 1); };
@@ -509,16 +512,16 @@ static int launch_attention(const float *q, const void *k, const void *v, float 
 }
 
 // The balanced split's shape for a mask-free call on the current device:
-// `parts` workgroups (one per CU) run `rounds` lockstep rounds of whole
-// units (of `nt` key tiles), then split the remaining units' `total` tiles
-// into equal ranges.  Returns false where that would not save tile steps
-// per CU against the plain grid's whole rounds (units a multiple of the CU
-// count, or too few split tiles for a part's merge to pay).  The CU count
-// is the current device's (256 when no device is visible).
+// `wgs` workgroups (one per CU) run `rounds` lockstep rounds of whole units
+// (of `nt` key tiles), then the remaining units' `total` tiles are split
+// into `parts` equal ranges.  Returns false where that would not pay (see
+// below).  The CU count is the current device's (256 when no device is
+// visible).
 struct AttSplit {
     long long units, total;
-    int nt, nqb, parts, rounds;
+    int nt, nqb, wgs, parts, rounds;
 };
+
 static bool attention_split(int queries, int keys, int heads, AttSplit &sp) {
     if (queries <= 0 || keys <= 0) return false;
     const int cus = device_cus();
@@ -531,16 +534,22 @@ static bool attention_split(int queries, int keys, int heads, AttSplit &sp) {
     // Every range must hold at least one tile (so each unit's parts are
     // exactly the ranges r_first..r_last): one part per tile when there
     // are fewer tiles than CUs and no whole rounds.
-    sp.parts = cus;
-    if (sp.total < cus) {
-        if (sp.rounds > 0 || sp.total == 0) return false;
-        sp.parts = static_cast<int>(sp.total);
-    }
-    const long long plain = (sp.units + cus - 1) / cus * sp.nt;
-    const long long split = sp.rounds * static_cast<long long>(sp.nt) + (sp.total + sp.parts - 1) / sp.parts;
-    // Charge each range two tile steps for its merges; take the split only
-    // where it saves at least 5 % of the plain grid's steps.
-    return (split + 2) * 100 <= plain * 95;
+    if (sp.total == 0) return false;
+    // Parts of at least 8 tiles (fewer parts for a merge to read), at most
+    // one range per CU.
+    sp.parts = static_cast<int>(min(static_cast<long long>(cus), max(1LL, sp.total / 8)));
+    sp.wgs = sp.rounds > 0 ? cus : sp.parts;
+    // The split tail runs at about 60 % of a lockstep round's efficiency
+    // (its ranges read the key tiles at scattered phases, and parts merge
+    // through memory), so it pays only where it needs at most 60 % of a
+    // round's tile steps, charging each range two steps for its merges:
+    // the plain grid's last round is then about half empty or less.
+    // Measured at 4352 tokens (us, plain -> split): 8 heads 117 -> 102,
+    // 16 heads 254 -> 197, 20 heads 252 -> 221, 32 heads 404 -> 343, 48
+    // heads 551 -> 509; left plain: 12 heads 132 (split 142), 24 heads 256
+    // (257), 28 heads 283 (295), 40 heads 410 (421).
+    const long long per_part = (sp.total + sp.parts - 1) / sp.parts;
+    return (per_part + 2) * 100 <= 60LL * sp.nt;
 }
 
 static long long attention_workspace(int queries, int keys, int heads) {
@@ -572,9 +581,9 @@ static int launch_attention_ws(const float *q, const void *k, const void *v, flo
     att_clear_kernel<<<static_cast<unsigned>((sp.units + 255) / 256), 256, 0, stream>>>(arrivals,
                                                                                        static_cast<int>(sp.units));
     if (const int e = launch_status()) return e;
-    flash_attention_stream_kernel<<<sp.parts, dim3(ATT_THREADS), 0, stream>>>(
+    flash_attention_stream_kernel<<<sp.wgs, dim3(ATT_THREADS), 0, stream>>>(
         q, static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v), out, queries, keys, heads, arrivals,
-        part_ml, part_o, sp.rounds, sp.total, sp.nt, sp.nqb);
+        part_ml, part_o, sp.rounds, sp.total, sp.nt, sp.nqb, sp.parts);
     return launch_status();
 }
 

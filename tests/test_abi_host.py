@@ -235,19 +235,24 @@ def _att_split_bytes(units, parts):
 
 
 @pytest.mark.parametrize("nq,nk,heads,parts", [
-    (4352, 4352, 24, 256),      # 408 query blocks: one lockstep round, 152 blocks split
-    (4352, 4352, 8, 256),       # 136 query blocks: all split
-    (129, 1000, 2, 32),         # 2 blocks x 16 key tiles: one part per tile
-    (4352, 4352, 15, None),     # 255 blocks: one round already
-    (4352, 4352, 30, None),     # 510 blocks: the split would not save 5 %
+    (4352, 4352, 16, 136),      # 272 query blocks: one lockstep round, 16 blocks split in 8-tile parts
+    (4352, 4352, 20, 256),      # 340 blocks: 84 split over every CU
+    (4352, 4352, 48, 256),      # 816 blocks: three rounds, 48 split
+    (4352, 4352, 8, 256),       # 136 blocks: no whole round, all split
+    (300, 4100, 3, 48),         # 6 blocks x 65 key tiles: 8-tile parts
+    (4352, 4352, 24, None),     # 408 blocks: the last round 59 % full, left plain
+    (4352, 4352, 12, None),     # 204 blocks in one round
+    (4352, 4352, 30, None),     # 510 blocks
     (256 * 256, 4352, 1, None), # exactly one round
+    (129, 1000, 2, None),       # 16 key tiles: parts too short for their merges
     (0, 64, 1, None), (64, 0, 1, None), (64, 64, 0, None),
 ])
 def test_attention_split_choice(nq, nk, heads, parts):
     """The attention's balanced split (qi_hip_flash_attention_ws) and its
     workspace at a 256-CU device's rule (the library's default when no GPU
-    is visible): taken where whole rounds of 256-query blocks would leave CUs
-    idle for at least 5 % of the plain grid's tile steps."""
+    is visible): whole rounds of 256-query blocks in lockstep, then the rest
+    in ranges of at least 8 key tiles, taken only where a range needs at
+    most 60 % of a round's tile steps (two charged for its merges)."""
     got = qwen_image_hip.load().qi_hip_flash_attention_workspace_bytes(nq, nk, heads)
     units = -(-nq // 256) * heads
     assert got == (0 if parts is None else _att_split_bytes(units, parts))
