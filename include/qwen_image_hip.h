@@ -306,15 +306,16 @@ int qi_flash_attention(const float *q, const void *k_half, const void *v_half, f
 int qi_hip_flash_attention(const float *q, const void *k_half, const void *v_half, float *out, int queries, int keys,
                            int heads, int query_offset, int causal_rows, const int *visible_keys, void *stream);
 /* The attention above with a caller workspace.  A call in which every row
- * sees every key (visible_keys NULL and causal_rows <= query_offset)
- * balances the work over one workgroup per CU: each walks an equal share
- * of the (head, 256-query block, 64-key tile) sequence, and where a
- * workgroup's share ends inside a query block, its O, offset and sum go to
- * the workspace and the block's last part to finish merges the parts in
- * workgroup order (so results do not depend on timing).  Outputs agree
- * with qi_hip_flash_attention within the attention tolerance.  Masked
- * calls, calls the split would not speed up (query blocks a multiple of the
- * CU count), and calls with less than
+ * sees every key (visible_keys NULL and causal_rows <= query_offset) and
+ * whose (head, 256-query block) units would leave the last round of CUs
+ * about half empty or more runs the whole rounds in lockstep, one
+ * workgroup per CU, then splits the remaining units' 64-key tiles into
+ * equal ranges of at least 8 tiles; where a range ends inside a query
+ * block, its O, offset and sum go to the workspace and the block's last
+ * part to finish merges the parts in range order (so results do not
+ * depend on timing).  Outputs agree with qi_hip_flash_attention within the
+ * attention tolerance.  Masked calls, calls the split would not speed up,
+ * and calls with less than
  * qi_hip_flash_attention_workspace_bytes(queries, keys, heads) run as
  * qi_hip_flash_attention does.  workspace: 16-byte aligned device memory
  * used only while the call's kernels run on `stream` (calls on one stream

@@ -29,13 +29,14 @@
 // hold one query each, so the online rescaling is lane-local.
 //
 // Balanced split (flash_attention_stream_kernel, mask-free calls with a
-// workspace).  One workgroup fills a CU, so 17 query blocks x 24 heads =
-// 408 workgroups run as 1.6 rounds on 256 CUs.  Instead one workgroup per CU
-// walks an equal share of the (unit, key tile) sequence, units = (head,
-// query block) in head-major order; a unit cut between workgroups leaves
-// each part's O^T, offset and sum in the workspace, and the part that
-// arrives last (an arrival counter per unit) merges them in workgroup order,
-// so the result does not depend on timing.
+// workspace).  One workgroup fills a CU, so the grid of (head, query block)
+// units runs in whole rounds of CUs, and a mostly empty last round (4352
+// tokens x 16 heads: 272 units on 256 CUs) costs nearly a full one.  The
+// split runs the whole rounds in lockstep, one workgroup per CU, then cuts
+// the remaining units' key tiles into equal ranges; a unit cut between
+// workgroups leaves each part's O^T, offset and sum in the workspace, and
+// the part that arrives last (an arrival counter per unit) merges them in
+// range order, so the result does not depend on timing.
 
 #include "qi_common.h"
 
