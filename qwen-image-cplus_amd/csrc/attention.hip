@@ -374,15 +374,14 @@ __global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_kernel(
     att_store(out, o, l_run, queries, heads, head, qblk);
 }
 
-// Workspace of the balanced split for `parts` workgroups and `units` units:
-// the arrival counters, then per workgroup two part slots (the unit its
-// split range starts in, the unit it ends in) of offsets and sums (float2
-// per thread) and O^T (64 floats per thread, register-major so that each
-// access of a wave is 256 contiguous bytes).
+// Workspace of the balanced split for `tail` split units of `segs` parts:
+// the arrival counters (one per split unit), then per part its offsets and
+// sums (two floats per thread) and O^T (64 floats per thread,
+// register-major so that each access of a wave is 256 contiguous bytes).
 constexpr int ATT_THREADS = ATT_WAVES * WAVE;
-inline size_t att_counter_bytes(long long units) { return (static_cast<size_t>(units) * 4 + 255) / 256 * 256; }
-inline size_t att_split_bytes(long long units, int parts) {
-    return att_counter_bytes(units) + static_cast<size_t>(2 * parts) * ATT_THREADS * (8 + 64 * 4);
+inline size_t att_counter_bytes(long long tail) { return (static_cast<size_t>(tail) * 4 + 255) / 256 * 256; }
+inline size_t att_split_bytes(long long tail, int segs) {
+    return att_counter_bytes(tail) + static_cast<size_t>(tail) * segs * ATT_THREADS * (8 + 64 * 4);
 }
 
 __global__ void att_clear_kernel(unsigned *__restrict__ counters, int n) {
@@ -405,13 +404,13 @@ __device__ __forceinline__ float att_get(const float *p) {
 // One workgroup per CU.  First `rounds` rounds of whole units in lockstep
 // (unit i * gridDim.x + r in round i: the workgroups of an XCD then read
 // the same key tiles of the same heads at the same time, as the plain grid
-// does), then the remaining units' key tiles split into `parts` equal
-// ranges, run by ranges 0 .. parts - 1.
+// does), then the remaining `tail` units, each cut into `segs` aligned
+// segments of `seg_len` key tiles, as parts dealt out in the same way.
 __global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_stream_kernel(
     const float *__restrict__ q, const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     float *__restrict__ out, int queries, int keys, int heads, unsigned *__restrict__ arrivals,
-    float *__restrict__ part_ml, float *__restrict__ part_o, int rounds, long long total, int nt, int nqb,
-    int parts) {
+    float *__restrict__ part_ml, float *__restrict__ part_o, int rounds, int tail, int nt, int nqb, int segs,
+    int seg_len) {
     __shared__ AttLds lds;
     const int tid = threadIdx.x;
     const int wgs = gridDim.x;
@@ -426,57 +425,47 @@ __global__ __launch_bounds__(ATT_WAVES *WAVE, 1) void flash_attention_stream_ker
         att_keys(q, k, v, queries, keys, heads, u / nqb, u % nqb, 0, keys, keys, keys, lds, o, m_run, l_run);
         att_store(out, o, l_run, queries, heads, u / nqb, u % nqb);
     }
-    if (r >= parts) return;              // the split tail runs on ranges 0 .. parts - 1
-    const int ubase = rounds * wgs;  // first split unit; t counts its tiles on
-    auto bound = [&](int rr) { return static_cast<long long>(rr) * total / parts; };
-    // The range holding split tile t: the largest rr with bound(rr) <= t.
-    auto owner = [&](long long t) { return static_cast<int>(((t + 1) * parts + total - 1) / total - 1); };
-    const long long t0 = bound(r), t1 = bound(r + 1);
-    for (long long t = t0; t < t1;) {
-        const int us = static_cast<int>(t / nt);
-        const int tb = static_cast<int>(t - static_cast<long long>(us) * nt);
-        const int te = static_cast<int>(min(static_cast<long long>(nt), tb + (t1 - t)));
-        const int u = ubase + us, head = u / nqb, qblk = u % nqb;
+    // The tail: each remaining unit cut into `segs` segments of `seg_len`
+    // key tiles; part p = seg * tail + unit (segment-major, so that the
+    // workgroups of an XCD take consecutive parts: the same segment of the
+    // same heads' units, the same key tiles at the same time).
+    const int ubase = rounds * wgs;
+    const int nparts = tail * segs;
+    for (int p = r; p < nparts; p += wgs) {
+        const int seg = p / tail, ut = p - seg * tail, u = ubase + ut;
+        const int head = u / nqb, qblk = u % nqb;
+        const int tb = seg * seg_len, te = min(nt, tb + seg_len);
         v16f_t o[4];
         float m_run, l_run;
         att_keys(q, k, v, queries, keys, heads, head, qblk, tb * ATT_KT, min(te * ATT_KT, keys), keys, keys, lds, o,
                  m_run, l_run);
-        t += te - tb;
-        if (tb == 0 && te == nt) {
-            att_store(out, o, l_run, queries, heads, head, qblk);
-            continue;
-        }
-        // A part of unit u: ranges r_first..r_last hold its parts, range rr
-        // in slot 2 rr when its range starts inside u, else 2 rr + 1.
-        const long long ubegin = static_cast<long long>(us) * nt;
-        const int r_first = owner(ubegin), r_last = owner(ubegin + nt - 1);
-        auto slot = [&](int rr) { return bound(rr) >= ubegin ? 2 * rr : 2 * rr + 1; };
-        const int own = slot(r);
-        att_put(part_ml + (2 * own) * ATT_THREADS + tid, m_run);
-        att_put(part_ml + (2 * own + 1) * ATT_THREADS + tid, l_run);
-        float *po = part_o + static_cast<size_t>(own) * 64 * ATT_THREADS + tid;
+        // Part p in slot p; the unit's last part to arrive merges them.
+        att_put(part_ml + (2 * p) * ATT_THREADS + tid, m_run);
+        att_put(part_ml + (2 * p + 1) * ATT_THREADS + tid, l_run);
+        float *po = part_o + static_cast<size_t>(p) * 64 * ATT_THREADS + tid;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) att_put(po + (16 * j + e) * ATT_THREADS, o[j][e]);
         // Every thread's stores complete (acknowledged at the coherent
-        // level), then one arrival; the part that arrives last merges.
+        // level), then one arrival.
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (tid == 0)
-            lds.last = __hip_atomic_fetch_add(&arrivals[u], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                       static_cast<unsigned>(r_last - r_first);
+            lds.last = __hip_atomic_fetch_add(&arrivals[ut], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                       static_cast<unsigned>(segs - 1);
         __syncthreads();
         if (!lds.last) continue;
         float mx = -__builtin_inff();
-        for (int rr = r_first; rr <= r_last; ++rr) mx = fmaxf(mx, att_get(part_ml + (2 * slot(rr)) * ATT_THREADS + tid));
+        for (int sg = 0; sg < segs; ++sg)
+            mx = fmaxf(mx, att_get(part_ml + (2 * (sg * tail + ut)) * ATT_THREADS + tid));
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) o[j][e] = 0.f;
         float l_sum = 0.f;
-        for (int rr = r_first; rr <= r_last; ++rr) {
-            const int sl = slot(rr);
+        for (int sg = 0; sg < segs; ++sg) {
+            const int sl = sg * tail + ut;
             const float m_s = att_get(part_ml + (2 * sl) * ATT_THREADS + tid);
             const float w = m_s == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m_s - mx);
             l_sum += w * att_get(part_ml + (2 * sl + 1) * ATT_THREADS + tid);
@@ -514,49 +503,54 @@ static int launch_attention(const float *q, const void *k, const void *v, float 
 
 // The balanced split's shape for a mask-free call on the current device:
 // `wgs` workgroups (one per CU) run `rounds` lockstep rounds of whole units
-// (of `nt` key tiles), then the remaining units' `total` tiles are split
-// into `parts` equal ranges.  Returns false where that would not pay (see
-// below).  The CU count is the current device's (256 when no device is
-// visible).
+// (of `nt` key tiles), then the remaining `tail` units as `segs` aligned
+// segments of `seg_len` tiles each.  Returns false where that would not
+// pay (see below).  The CU count is the current device's (256 when no
+// device is visible).
 struct AttSplit {
-    long long units, total;
-    int nt, nqb, wgs, parts, rounds;
+    long long units;
+    int nt, nqb, wgs, rounds, tail, segs, seg_len;
 };
-
 static bool attention_split(int queries, int keys, int heads, AttSplit &sp) {
     if (queries <= 0 || keys <= 0) return false;
     const int cus = device_cus();
     sp.nqb = (queries + ATT_QB - 1) / ATT_QB;
     sp.nt = (keys + ATT_KT - 1) / ATT_KT;
     sp.units = static_cast<long long>(sp.nqb) * heads;
-    if (sp.units >= (1ll << 31) || sp.units * sp.nt >= (1ll << 40)) return false;
+    if (sp.units >= (1ll << 31) || sp.nt < 4) return false;
     sp.rounds = static_cast<int>(sp.units / cus);
-    sp.total = (sp.units - static_cast<long long>(sp.rounds) * cus) * sp.nt;
-    // Every range must hold at least one tile (so each unit's parts are
-    // exactly the ranges r_first..r_last): one part per tile when there
-    // are fewer tiles than CUs and no whole rounds.
-    if (sp.total == 0) return false;
-    // Parts of at least 8 tiles (fewer parts for a merge to read), at most
-    // one range per CU.
-    sp.parts = static_cast<int>(min(static_cast<long long>(cus), max(1LL, sp.total / 8)));
-    sp.wgs = sp.rounds > 0 ? cus : sp.parts;
-    // The split tail runs at about 60 % of a lockstep round's efficiency
-    // (its ranges read the key tiles at scattered phases, and parts merge
-    // through memory), so it pays only where it needs at most 60 % of a
-    // round's tile steps, charging each range two steps for its merges:
-    // the plain grid's last round is then about half empty or less.
-    // Measured at 4352 tokens (us, plain -> split): 8 heads 117 -> 102,
-    // 16 heads 254 -> 197, 20 heads 252 -> 221, 32 heads 404 -> 343, 48
-    // heads 551 -> 509; left plain: 12 heads 132 (split 142), 24 heads 256
-    // (257), 28 heads 283 (295), 40 heads 410 (421).
-    const long long per_part = (sp.total + sp.parts - 1) / sp.parts;
-    return (per_part + 2) * 100 <= 60LL * sp.nt;
+    sp.tail = static_cast<int>(sp.units - static_cast<long long>(sp.rounds) * cus);
+    sp.wgs = cus;
+    if (sp.tail == 0) return false;
+    // The segment count with the fewest tile steps per CU for the tail, its
+    // parts all in one round of CUs (a part has fixed costs -- its Q
+    // fragments, the first tile's latency, its store and merge -- that made
+    // several rounds of parts slower than the plain grid: 4352 tokens x 24
+    // heads 251 -> 271 us in three rounds of 14-tile parts): the segment
+    // length, plus one tile step per part beyond the first for the merge
+    // that reads it; at most 16 segments.
+    long long best = -1;
+    for (int s = 2; s <= 16 && s <= sp.nt && static_cast<long long>(sp.tail) * s <= cus; ++s) {
+        const int len = (sp.nt + s - 1) / s, segs = (sp.nt + len - 1) / len;
+        const long long cost = len + (segs - 1);
+        if (best < 0 || cost < best) {
+            best = cost;
+            sp.segs = segs;
+            sp.seg_len = len;
+        }
+    }
+    if (best < 0 || static_cast<long long>(sp.tail) * sp.segs * ATT_THREADS * 264 >= (1ll << 40)) return false;
+    // Take it where the tail costs at most 85 % of the plain grid's extra
+    // round of whole units.  Measured at 4352 tokens (us, plain -> split):
+    // 16 heads 251 -> 187, 20 heads 250 -> 212, 32 heads 397 -> 343, 48
+    // heads 541 -> 487; 24 heads (152 tail units) stay plain at 251.
+    return best * 100 <= 85LL * sp.nt;
 }
 
 static long long attention_workspace(int queries, int keys, int heads) {
     AttSplit sp;
     if (!attention_split(queries, keys, heads, sp)) return 0;
-    return static_cast<long long>(att_split_bytes(sp.units, sp.parts));
+    return static_cast<long long>(att_split_bytes(sp.tail, sp.segs));
 }
 
 static int launch_attention_ws(const float *q, const void *k, const void *v, float *out, int queries, int keys,
@@ -569,22 +563,21 @@ static int launch_attention_ws(const float *q, const void *k, const void *v, flo
     // no causal row among these rows.
     const bool mask_free = visible_keys == nullptr && causal_rows <= query_offset;
     if (!mask_free || !workspace || !attention_split(queries, keys, heads, sp) ||
-        workspace_bytes < static_cast<long long>(att_split_bytes(sp.units, sp.parts)))
+        workspace_bytes < static_cast<long long>(att_split_bytes(sp.tail, sp.segs)))
         return launch_attention(q, k, v, out, queries, keys, heads, query_offset, causal_rows, visible_keys,
                                 stream);
     auto *base = static_cast<unsigned char *>(workspace);
     auto *arrivals = reinterpret_cast<unsigned *>(base);
-    auto *part_ml = reinterpret_cast<float *>(base + att_counter_bytes(sp.units));
-    auto *part_o = reinterpret_cast<float *>(base + att_counter_bytes(sp.units) +
-                                             static_cast<size_t>(2 * sp.parts) * ATT_THREADS * 8);
+    auto *part_ml = reinterpret_cast<float *>(base + att_counter_bytes(sp.tail));
+    auto *part_o = reinterpret_cast<float *>(base + att_counter_bytes(sp.tail) +
+                                             static_cast<size_t>(sp.tail) * sp.segs * ATT_THREADS * 8);
     // The counters start at zero on every call (a fill kernel, not a memset,
     // so the pair can sit in a captured graph).
-    att_clear_kernel<<<static_cast<unsigned>((sp.units + 255) / 256), 256, 0, stream>>>(arrivals,
-                                                                                       static_cast<int>(sp.units));
+    att_clear_kernel<<<static_cast<unsigned>((sp.tail + 255) / 256), 256, 0, stream>>>(arrivals, sp.tail);
     if (const int e = launch_status()) return e;
     flash_attention_stream_kernel<<<sp.wgs, dim3(ATT_THREADS), 0, stream>>>(
         q, static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v), out, queries, keys, heads, arrivals,
-        part_ml, part_o, sp.rounds, sp.total, sp.nt, sp.nqb, sp.parts);
+        part_ml, part_o, sp.rounds, sp.tail, sp.nt, sp.nqb, sp.segs, sp.seg_len);
     return launch_status();
 }
 

@@ -228,31 +228,33 @@ def test_cplus_binding_matches_the_header():
     assert cplus["qi_f32_to_f16"] == ([("source", "*f32"), ("out", "*u8"), ("count", "u64")], "i32")
 
 
-def _att_split_bytes(units, parts):
-    """Counters (4 bytes per unit, 256-byte rounded), then two part slots per
-    workgroup of 512 threads x (offset, sum, 64 O floats)."""
-    return (units * 4 + 255) // 256 * 256 + 2 * parts * 512 * (8 + 256)
+def _att_split_bytes(tail, segs):
+    """Counters (4 bytes per split unit, 256-byte rounded), then one part
+    slot per segment of each split unit: 512 threads x (offset, sum, 64 O
+    floats)."""
+    return (tail * 4 + 255) // 256 * 256 + tail * segs * 512 * (8 + 256)
 
 
-@pytest.mark.parametrize("nq,nk,heads,parts", [
-    (4352, 4352, 16, 136),      # 272 query blocks: one lockstep round, 16 blocks split in 8-tile parts
-    (4352, 4352, 20, 256),      # 340 blocks: 84 split over every CU
-    (4352, 4352, 48, 256),      # 816 blocks: three rounds, 48 split
-    (4352, 4352, 8, 256),       # 136 blocks: no whole round, all split
-    (300, 4100, 3, 48),         # 6 blocks x 65 key tiles: 8-tile parts
-    (4352, 4352, 24, None),     # 408 blocks: the last round 59 % full, left plain
-    (4352, 4352, 12, None),     # 204 blocks in one round
-    (4352, 4352, 30, None),     # 510 blocks
-    (256 * 256, 4352, 1, None), # exactly one round
-    (129, 1000, 2, None),       # 16 key tiles: parts too short for their merges
-    (0, 64, 1, None), (64, 0, 1, None), (64, 64, 0, None),
+@pytest.mark.parametrize("nq,nk,heads,tail,segs", [
+    (4352, 4352, 16, 16, 7),    # 272 query blocks: one lockstep round, 16 left in 7 segments
+    (4352, 4352, 20, 84, 3),    # 340 blocks: 84 left in 3 segments (252 parts, one round of CUs)
+    (4352, 4352, 32, 32, 7),    # 544 blocks: two rounds, 32 left
+    (4352, 4352, 48, 48, 5),    # 816 blocks: three rounds, 48 left
+    (300, 4100, 3, 6, 6),       # 6 blocks x 65 key tiles, no whole round
+    (129, 1000, 2, 2, 4),       # 2 blocks x 16 key tiles
+    (4352, 4352, 24, 0, 0),     # 408 blocks: 152 left would need parts over several rounds
+    (4352, 4352, 8, 0, 0),      # 136 blocks: likewise
+    (4352, 4352, 12, 0, 0),     # 204 blocks in one round
+    (256 * 256, 4352, 1, 0, 0), # exactly one round
+    (129, 192, 2, 0, 0),        # 3 key tiles: too short to split
+    (0, 64, 1, 0, 0), (64, 0, 1, 0, 0), (64, 64, 0, 0, 0),
 ])
-def test_attention_split_choice(nq, nk, heads, parts):
+def test_attention_split_choice(nq, nk, heads, tail, segs):
     """The attention's balanced split (qi_hip_flash_attention_ws) and its
     workspace at a 256-CU device's rule (the library's default when no GPU
-    is visible): whole rounds of 256-query blocks in lockstep, then the rest
-    in ranges of at least 8 key tiles, taken only where a range needs at
-    most 60 % of a round's tile steps (two charged for its merges)."""
+    is visible): whole rounds of 256-query blocks in lockstep, then the
+    `tail` blocks left, each cut into `segs` aligned key segments, all parts
+    in one round of CUs; taken where the tail costs at most 85 % of a round
+    of whole blocks."""
     got = qwen_image_hip.load().qi_hip_flash_attention_workspace_bytes(nq, nk, heads)
-    units = -(-nq // 256) * heads
-    assert got == (0 if parts is None else _att_split_bytes(units, parts))
+    assert got == (_att_split_bytes(tail, segs) if tail else 0)

@@ -115,17 +115,18 @@ def test_attention_split_choice(dev):
     assert _split_bytes(256 * (cus + cus // 16), 4352, 1) > 0  # one round and 1/16 of another
     assert _split_bytes(256 * cus, 4352, 1) == 0               # exactly one round
     assert _split_bytes(300, 4100, 3) > 0                      # 6 blocks: keys spread over CUs
-    assert _split_bytes(129, 1000, 2) == 0                     # 16 key tiles: too short to split
+    assert _split_bytes(129, 192, 2) == 0                      # 3 key tiles: too short to split
+    assert _split_bytes(4352, 4352, 24) == 0                   # 152 blocks left: parts over several rounds
     assert _split_bytes(0, 1000, 2) == 0 and _split_bytes(10, 0, 2) == 0
     assert _split_bytes(10, 10, 0) == 0
 
 
 @pytest.mark.parametrize("nq,nk,heads,offset", [(2000, 2100, 40, 0), (300, 4100, 3, 0), (1000, 2000, 5, 64)])
 def test_attention_split_vs_oracle(dev, nq, nk, heads, offset):
-    """A lockstep round then split query blocks, query blocks split in
-    eight parts, ragged key and query tiles, and a query offset with no
-    causal row: the balanced split against the oracle and against the
-    one-block-per-workgroup grid."""
+    """A lockstep round then the blocks left split in 4 key segments, 6
+    blocks in 6 segments with ragged key and query tiles, and a query
+    offset with no causal row: the balanced split against the oracle and
+    against the one-block-per-workgroup grid."""
     print(f"attention split nq={nq} nk={nk} heads={heads} offset={offset}", flush=True)
     assert _split_bytes(nq, nk, heads) > 0
     q, k, v = _case(nq, nk, heads, 1500 + nq)
