@@ -307,13 +307,12 @@ int qi_hip_flash_attention(const float *q, const void *k_half, const void *v_hal
                            int heads, int query_offset, int causal_rows, const int *visible_keys, void *stream);
 /* The attention above with a caller workspace.  A call in which every row
  * sees every key (visible_keys NULL and causal_rows <= query_offset) and
- * whose (head, 256-query block) units would leave the last round of CUs
- * about half empty or more runs the whole rounds in lockstep, one
- * workgroup per CU, then splits the remaining units' 64-key tiles into
- * equal ranges of at least 8 tiles; where a range ends inside a query
- * block, its O, offset and sum go to the workspace and the block's last
- * part to finish merges the parts in range order (so results do not
- * depend on timing).  Outputs agree with qi_hip_flash_attention within the
+ * whose (head, 256-query block) units leave a last round of CUs that its
+ * units, each cut into 2-16 aligned key segments, fill in one round of
+ * parts runs the whole rounds in lockstep, one workgroup per CU, then
+ * those parts; each part's O, offset and sum go to the workspace and the
+ * block's last part to finish merges them in segment order (so results
+ * do not depend on timing).  Outputs agree with qi_hip_flash_attention within the
  * attention tolerance.  Masked calls, calls the split would not speed up,
  * and calls with less than
  * qi_hip_flash_attention_workspace_bytes(queries, keys, heads) run as

@@ -33,10 +33,10 @@
 // units runs in whole rounds of CUs, and a mostly empty last round (4352
 // tokens x 16 heads: 272 units on 256 CUs) costs nearly a full one.  The
 // split runs the whole rounds in lockstep, one workgroup per CU, then cuts
-// the remaining units' key tiles into equal ranges; a unit cut between
-// workgroups leaves each part's O^T, offset and sum in the workspace, and
-// the part that arrives last (an arrival counter per unit) merges them in
-// range order, so the result does not depend on timing.
+// each remaining unit into aligned key segments, its parts dealt out one
+// per CU; each part leaves its O^T, offset and sum in the workspace, and
+// the unit's part that arrives last (an arrival counter per unit) merges
+// them in segment order, so the result does not depend on timing.
 
 #include "qi_common.h"
 
