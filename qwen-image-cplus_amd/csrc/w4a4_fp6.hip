@@ -365,16 +365,17 @@ __device__ __forceinline__ void fp6_tiles(uint8_t *lds, const uint8_t *__restric
             constexpr int q = decltype(qc)::value;
             if constexpr (q < T) {
                 constexpr int i = q / TN, j = q % TN;
-                tile_fma(j, i);
-                __builtin_amdgcn_sched_barrier(0);
-                // The next group's DMA loads go out one per tile step so their
-                // issue cost overlaps the MFMA chain instead of stalling it at
-                // the group's start; the vmcnt wait per group is unchanged.
+                // The next group's DMA loads go out one per tile step, ahead
+                // of the step's fp32 work, so their issue cost overlaps the
+                // MFMA chain instead of stalling it at the group's start;
+                // the vmcnt wait per group is unchanged.
                 if constexpr (q < L_PER_W) issue_one(gload, u, q);
                 if constexpr (q == T - 1) {
 #pragma unroll
                     for (int uu = T; uu < L_PER_W; ++uu) issue_one(gload, u, uu);
                 }
+                __builtin_amdgcn_sched_barrier(0);
+                tile_fma(j, i);
                 __builtin_amdgcn_sched_barrier(0);
                 // sp[i] is free once the last tile of row tile i has
                 // stepped.
