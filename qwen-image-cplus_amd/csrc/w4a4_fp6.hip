@@ -239,9 +239,11 @@ __device__ __forceinline__ void fp6_tiles(uint8_t *lds, const uint8_t *__restric
         v32f z32;
 #pragma unroll
         for (int r = 0; r < 32; ++r) z32[r] = 0.f;
-        // Issued at raised wave priority (also the partial tiles below), so
-        // the matrix core's next instruction wins issue over the other
-        // wave's vector work: measured 2-3 % faster on MI355X.
+        // Issued at raised wave priority, so the matrix core's next
+        // instruction wins issue over the other wave's vector work:
+        // measured 2-3 % faster on MI355X.  The partial tiles below run at
+        // normal priority: with the loads spread over the tile steps,
+        // raising it for them too measured 2-3 % slower.
 #ifdef QI_ABLATE_MFMA
         asm volatile("" : "+v"(sp[i]));
         return;
@@ -260,9 +262,7 @@ __device__ __forceinline__ void fp6_tiles(uint8_t *lds, const uint8_t *__restric
         asm volatile("" : "+v"(p[j][i]));
         return;
 #endif
-        __builtin_amdgcn_s_setprio(1);
         p[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(F.wf[j], F.xf[i], z, 2, 2, 0, 127, 0, 127);
-        __builtin_amdgcn_s_setprio(0);
     };
     // The exact fp32 step of one tile and group, in ascending group order.
     auto tile_fma = [&](int j, int i) {
